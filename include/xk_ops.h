@@ -1,0 +1,94 @@
+/*
+ * xk_ops.h -- C-ABI of the MI355X (gfx950) kernels behind the xLLM
+ * Triton-Ascend op set (reference: Fengfengst123/torch_npu_ops, triton_npu/).
+ *
+ * This ABI replaces the reference's launch runtime: the `.npubin` loader
+ * (triton_npu/kernel_registry.cpp:112-296), the packed-argument blob
+ * (triton_npu/args_builder.h:34-302) and OperationBase::execute
+ * (triton_npu/operation_base.h:136-192).  Every function here
+ *   - takes raw device pointers, element strides, scalar parameters, dtype
+ *     enums and a hipStream_t passed as `void*`;
+ *   - returns 0 on success, a negative XK_ERR_* code for an argument the
+ *     kernels cannot take, or a positive hipError_t for a launch failure;
+ *   - never throws, never synchronises and never touches host memory;
+ *   - allocates nothing: where a kernel needs scratch memory the caller
+ *     passes a workspace whose size the matching *_workspace_bytes()
+ *     function reports (this replaces the JSON `workspace_size` field,
+ *     kernel_registry.cpp:55-107);
+ *   - launches only on the stream it is given, so it is safe under
+ *     hipGraph capture.
+ * All tensors are row-major.  "stride" arguments count elements, not bytes.
+ */
+#ifndef XK_OPS_H_
+#define XK_OPS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types understood by the kernels. */
+typedef enum xk_dtype {
+  XK_F32 = 0,
+  XK_BF16 = 1,
+  XK_F16 = 2,
+  XK_I32 = 3,
+  XK_I64 = 4
+} xk_dtype;
+
+/* Status codes (negative); positive values are hipError_t. */
+#define XK_OK 0
+#define XK_ERR_INVALID (-1)     /* shape / pointer / value the op rejects */
+#define XK_ERR_UNSUPPORTED (-2) /* dtype or configuration not built */
+#define XK_ERR_WORKSPACE (-3)   /* workspace missing or too small */
+
+const char* xk_version(void);
+const char* xk_status_string(int status);
+
+/* ------------------------------------------------------------------------
+ * a2. Grouped LayerNorm / RMSNorm forward with optional SiLU gate.
+ * Replaces xllm::kernel::npu::layer_norm_fwd
+ *   (triton_npu/torch_api/triton_ops_api.h:137-145,
+ *    npu_triton_layernorm_fwd.cpp:48-332)
+ * and npu_ops::layer_norm_fwd (ascendc_npu/ascendc_ops_api.h:31-39).
+ *   x, y, z : [M, N] rows with row strides; dtype `dtype` (f32/bf16/f16).
+ *   weight, bias : [N], dtype `wdtype`; bias and z may be NULL.
+ *   mean, rstd : fp32 [ngroups * M] at index group * M + row; mean is
+ *     ignored (may be NULL) when is_rms_norm, either may be NULL.
+ *   group_size divides N.  gate = z * sigmoid(z) is applied to y
+ *   (norm_before_gate != 0) or to x before the statistics.
+ */
+int xk_layer_norm_fwd(const void* x, int64_t stride_x_row, void* y,
+                      int64_t stride_y_row, const void* weight,
+                      const void* bias, const void* z, int64_t stride_z_row,
+                      float* mean, float* rstd, int64_t M, int64_t N,
+                      int64_t group_size, float eps, int norm_before_gate,
+                      int is_rms_norm, xk_dtype dtype, xk_dtype wdtype,
+                      void* stream);
+
+/* ------------------------------------------------------------------------
+ * a3. Gemma RMSNorm: y = x * rsqrt(mean(x^2) + eps) * (1 + gamma), fp32
+ * arithmetic, one statistic per row of N = gamma.numel() elements.
+ * Replaces npu_ops::npu_gemma_rms_norm (ascendc_npu/ascendc_ops_api.h:24-29,
+ * gemma_rms_norm.cpp:28-57).  rstd: fp32 [M] (may be NULL).
+ */
+int xk_gemma_rms_norm(const void* x, int64_t stride_x_row, void* y,
+                      int64_t stride_y_row, const void* gamma, float* rstd,
+                      int64_t M, int64_t N, float eps, xk_dtype dtype,
+                      xk_dtype wdtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * a6a. y = x * rsqrt(sum(x^2) + eps) over the last dim (contiguous rows).
+ * Replaces npu_l2norm_last_dim (triton_ops_api.h:31, npu_triton_l2norm.cpp).
+ */
+int xk_l2norm_last_dim(const void* x, void* y, int64_t rows, int64_t cols,
+                       float eps, xk_dtype dtype, xk_dtype out_dtype,
+                       void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* XK_OPS_H_ */

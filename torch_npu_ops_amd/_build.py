@@ -1,0 +1,92 @@
+"""Build recipes for the native parts of torch_npu_ops_amd.
+
+* ``libxk.so`` -- every HIP kernel plus the C-ABI of ``include/xk_ops.h``,
+  compiled by hipcc for gfx950 only.  No torch dependency.
+* ``_torch_api*.so`` -- the C++ drop-in layer (the reference's torch_api
+  signatures) linked against libtorch and libxk.so, with a pybind module for
+  tests.
+
+Both land in-tree next to this file so that they travel with the repository
+snapshot.  Objects go to ``torch_npu_ops_amd/_build/``.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import glob
+import os
+import shutil
+import subprocess
+import sys
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+REPO_DIR = os.path.dirname(PKG_DIR)
+CSRC_DIR = os.path.join(PKG_DIR, "csrc")
+INCLUDE_DIR = os.path.join(REPO_DIR, "include")
+BUILD_DIR = os.path.join(PKG_DIR, "_build")
+LIB_PATH = os.path.join(PKG_DIR, "libxk.so")
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# -packed-fp32-ops: keep the compiler from emitting v_pk_{add,mul,fma}_f32
+# (some forms have given silently wrong results on these boxes).
+HIP_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics",
+    "-Wno-unused-result",
+    f"-I{INCLUDE_DIR}",
+    f"-I{CSRC_DIR}",
+]
+
+
+def _run(cmd: list[str]) -> None:
+    proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                          text=True)
+    # hipcc's host pass warns that it does not know the packed-fp32 feature;
+    # that line is expected and filtered.
+    out = "\n".join(l for l in proc.stdout.splitlines()
+                    if "packed-fp32-ops" not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"command failed ({proc.returncode}): {' '.join(cmd)}\n{out}")
+    if out.strip():
+        print(out, file=sys.stderr)
+
+
+def hip_sources() -> list[str]:
+    return sorted(glob.glob(os.path.join(CSRC_DIR, "*.hip")))
+
+
+def build_lib(jobs: int | None = None, verbose: bool = True) -> str:
+    """Compile every csrc/*.hip for gfx950 and link libxk.so."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    srcs = hip_sources()
+    objs = [os.path.join(BUILD_DIR, os.path.basename(s) + ".o") for s in srcs]
+    jobs = jobs or min(8, os.cpu_count() or 4)
+
+    def compile_one(pair):
+        src, obj = pair
+        _run([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for obj in ex.map(compile_one, zip(srcs, objs)):
+            if verbose:
+                print(f"[xk build] compiled {os.path.basename(obj)}", flush=True)
+    tmp = LIB_PATH + ".tmp"
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
+    os.replace(tmp, LIB_PATH)
+    if verbose:
+        print(f"[xk build] linked {LIB_PATH}", flush=True)
+    return LIB_PATH
+
+
+def clean() -> None:
+    shutil.rmtree(BUILD_DIR, ignore_errors=True)
+
+
+if __name__ == "__main__":
+    build_lib()

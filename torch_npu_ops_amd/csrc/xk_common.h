@@ -1,0 +1,115 @@
+// Shared device helpers for the gfx950 kernels: element conversion, vector
+// memory access and wave64 / work-group reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "xk_ops.h"
+
+namespace xk {
+
+using bf16 = __bf16;
+using f16 = _Float16;
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------------------
+// Scalar conversion.  bf16/f16 -> f32 is exact; f32 -> bf16/f16 rounds to
+// nearest even (gfx950 has a native v_cvt_pk_bf16_f32 for the bf16 case).
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+  return static_cast<float>(v);
+}
+template <typename T>
+__device__ __forceinline__ T from_f32(float v) {
+  return static_cast<T>(v);
+}
+
+// Load one element whose dtype is only known at run time (used for small
+// parameter vectors such as weights and gates, never in a bandwidth loop).
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i,
+                                             xk_dtype dt) {
+  switch (dt) {
+    case XK_BF16:
+      return static_cast<float>(reinterpret_cast<const bf16*>(p)[i]);
+    case XK_F16:
+      return static_cast<float>(reinterpret_cast<const f16*>(p)[i]);
+    default:
+      return reinterpret_cast<const float*>(p)[i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Vector access: N consecutive elements moved as one aligned load/store.
+// ---------------------------------------------------------------------------
+template <typename T, int N>
+struct alignas(sizeof(T) * N) Vec {
+  T v[N];
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void load_vec_f32(const T* p, float (&out)[N]) {
+  Vec<T, N> t = *reinterpret_cast<const Vec<T, N>*>(p);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = to_f32(t.v[i]);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_vec_f32(T* p, const float (&in)[N]) {
+  Vec<T, N> t;
+#pragma unroll
+  for (int i = 0; i < N; ++i) t.v[i] = from_f32<T>(in[i]);
+  *reinterpret_cast<Vec<T, N>*>(p) = t;
+}
+
+// ---------------------------------------------------------------------------
+// Reductions.
+// ---------------------------------------------------------------------------
+// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float silu(float x) {
+  return x / (1.0f + __expf(-x));
+}
+
+__device__ __forceinline__ float sigmoid(float x) {
+  return 1.0f / (1.0f + __expf(-x));
+}
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? XK_OK : static_cast<int>(e);
+}
+
+inline bool aligned(const void* p, int bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) {
+  return (a + b - 1) / b;
+}
+
+inline int elem_bytes(xk_dtype dt) {
+  switch (dt) {
+    case XK_BF16:
+    case XK_F16:
+      return 2;
+    case XK_I64:
+      return 8;
+    default:
+      return 4;
+  }
+}
+
+inline bool is_float_dtype(xk_dtype dt) {
+  return dt == XK_F32 || dt == XK_BF16 || dt == XK_F16;
+}
+
+}  // namespace xk
