@@ -1,17 +1,21 @@
 #!/usr/bin/env python3
 """Benchmark of the xLLM op set on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--op NAME] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--op NAME] [--no-cpu] [--eager]
 
-One step = one call of the op on its BASELINE config with inputs already
-resident in HBM.  Rank 0 prints ONE JSON line:
-  value       achieved GB/s of the headline op (algorithmic bytes / time)
-  roofline    achieved / peak for the dominant kernel, from per-launch HIP
-              events recorded on the stream the kernels run on
+One step = one call of an op on its BASELINE config with inputs already
+resident in HBM.  The K timed calls are captured in one HIP graph and
+replayed back to back (launch overhead of the Python binding would
+otherwise dominate the microsecond-scale ops); HIP events on the stream the
+kernels run on bracket the replay.  Inputs rotate over several buffer sets
+whose total exceeds the 256 MB Infinity Cache, so timings see HBM.
+
+Rank 0 prints ONE JSON line:
+  value        achieved GB/s of the headline op (algorithmic bytes / time)
+  roofline     the headline kernel's achieved / peak
   cpu_baseline the oracle (CPU restatement of the reference) on host cores
-  ops         every op's line (config, us/call, GB/s or tokens/s, roofline)
-Inputs rotate over several buffer sets whose total exceeds the 256 MB
-Infinity Cache so that timings see HBM, not the cache.
+  ops          every op's line (config, us per call, GB/s or tokens/s,
+               roofline)
 """
 from __future__ import annotations
 
@@ -26,6 +30,7 @@ import torch
 
 HBM_PEAK_GBS = 8000.0
 ROTATE_BYTES = 1 << 30  # >= 1 GiB of distinct buffers per op
+MAX_SETS = 128
 CPU_THREADS = min(16, os.cpu_count() or 1)
 
 REPO = os.path.dirname(os.path.abspath(__file__))
@@ -33,34 +38,42 @@ if REPO not in sys.path:
     sys.path.insert(0, REPO)
 
 
-# ---------------------------------------------------------------------------
-# Op cases.  Each builds seeded inputs (on the CPU, copied to the GPU),
-# returns a GPU closure per buffer set, the algorithmic bytes per call and a
-# CPU closure for the baseline.
-# ---------------------------------------------------------------------------
-class Case:
-    name = ""
-    config = ""
-    dtype = "bf16"
-    algo_bytes = 0
-    kernel = ""
-
-    def sets(self, dev, n):  # -> list of callables
-        raise NotImplementedError
-
-    def cpu(self):  # -> (callable, sample description, scale to one call)
-        raise NotImplementedError
-
-
 def _randn(shape, gen, dtype, scale=1.0, shift=0.0):
     return (torch.randn(shape, generator=gen) * scale + shift).to(dtype)
+
+
+def _cur_stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ok(st, lib):
+    if st:
+        from torch_npu_ops_amd import _lib
+        raise RuntimeError(_lib.status_string(st))
+
+
+class Case:
+    """One BASELINE config.  sets(dev, n) returns n closures, each running
+    the op once on its own buffers (stream read at call time); cpu()
+    returns the CPU baseline closure, a description and the factor that
+    scales one closure call to one full config call."""
+    name = ""
+    config = ""
+    kernel = ""
+    algo_bytes = 0
+
+    def sets(self, dev, n):
+        raise NotImplementedError
+
+    def cpu(self):
+        raise NotImplementedError
 
 
 class LayerNormCase(Case):
     name = "layer_norm_fwd"
     config = ("config 2a: layer_norm_fwd bf16 x[16384,4096], group_size 4096, "
               "affine w~N(1,0.1) b~N(0,0.1), eps 1e-5, outputs y + fp32 mean/rstd")
-    kernel = "layer_norm_fwd_kernel"
+    kernel = "ln_tile_kernel"
     M, N = 16384, 4096
     # x + y (bf16) + mean/rstd (fp32) + w/b (bf16)
     algo_bytes = M * N * 2 * 2 + M * 4 * 2 + N * 2 * 2
@@ -73,7 +86,6 @@ class LayerNormCase(Case):
 
     def sets(self, dev, n):
         from torch_npu_ops_amd import _lib
-        from torch_npu_ops_amd.ops import _stream
         lib = _lib.lib()
         w, b = self.w.to(dev), self.b.to(dev)
         out = []
@@ -82,33 +94,28 @@ class LayerNormCase(Case):
             y = torch.empty_like(x)
             mean = torch.empty(self.M, dtype=torch.float32, device=dev)
             rstd = torch.empty(self.M, dtype=torch.float32, device=dev)
-            s = _stream(x)
 
-            def run(x=x, y=y, mean=mean, rstd=rstd, s=s):
-                st = lib.xk_layer_norm_fwd(
+            def run(x=x, y=y, mean=mean, rstd=rstd):
+                _ok(lib.xk_layer_norm_fwd(
                     x.data_ptr(), self.N, y.data_ptr(), self.N, w.data_ptr(),
                     b.data_ptr(), None, 0, mean.data_ptr(), rstd.data_ptr(),
                     self.M, self.N, self.N, 1e-5, 1, 0, _lib.XK_BF16,
-                    _lib.XK_BF16, s)
-                if st:
-                    raise RuntimeError(_lib.status_string(st))
+                    _lib.XK_BF16, _cur_stream()), lib)
             out.append(run)
         return out
 
     def cpu(self):
         from oracle import norm as on
         x, w, b = self.x, self.w, self.b
-
-        def run():
-            on.layer_norm_fwd(x, w, b, 1e-5)
-        return run, "full config 2a (16384x4096), fp32 math on bf16 input", 1.0
+        return (lambda: on.layer_norm_fwd(x, w, b, 1e-5),
+                "full config 2a (16384x4096), fp32 math on bf16 input", 1.0)
 
 
 class GemmaCase(Case):
     name = "gemma_rms_norm"
     config = ("config 2b: Gemma RMSNorm bf16 x[16384,4096], gamma~N(1,0.1) "
               "applied as (1+gamma), eps 1e-5, outputs y + fp32 rstd")
-    kernel = "layer_norm_fwd_kernel"
+    kernel = "ln_tile_kernel"
     M, N = 16384, 4096
     algo_bytes = M * N * 2 * 2 + M * 4 + N * 2
 
@@ -119,7 +126,6 @@ class GemmaCase(Case):
 
     def sets(self, dev, n):
         from torch_npu_ops_amd import _lib
-        from torch_npu_ops_amd.ops import _stream
         lib = _lib.lib()
         gamma = self.gamma.to(dev)
         out = []
@@ -127,63 +133,119 @@ class GemmaCase(Case):
             x = self.x.to(dev)
             y = torch.empty_like(x)
             rstd = torch.empty(self.M, dtype=torch.float32, device=dev)
-            s = _stream(x)
 
-            def run(x=x, y=y, rstd=rstd, s=s):
-                st = lib.xk_gemma_rms_norm(
+            def run(x=x, y=y, rstd=rstd):
+                _ok(lib.xk_gemma_rms_norm(
                     x.data_ptr(), self.N, y.data_ptr(), self.N,
                     gamma.data_ptr(), rstd.data_ptr(), self.M, self.N, 1e-5,
-                    _lib.XK_BF16, _lib.XK_BF16, s)
-                if st:
-                    raise RuntimeError(_lib.status_string(st))
+                    _lib.XK_BF16, _lib.XK_BF16, _cur_stream()), lib)
             out.append(run)
         return out
 
     def cpu(self):
         from oracle import norm as on
         x, gamma = self.x, self.gamma
-
-        def run():
-            on.gemma_rms_norm(x, gamma, 1e-5)
-        return run, "full config 2b (16384x4096), fp32 math on bf16 input", 1.0
+        return (lambda: on.gemma_rms_norm(x, gamma, 1e-5),
+                "full config 2b (16384x4096), fp32 math on bf16 input", 1.0)
 
 
-CASES = {c.name: c for c in (LayerNormCase, GemmaCase)}
+class RopeCase(Case):
+    name = "split_rmsnorm_rope"
+    config = ("config 1: split q/k RMSNorm + neox RoPE fp32, 256 tokens, 32 q + "
+              "8 kv heads, head_dim 128, eps 1e-6, theta 1e6, sin/cos rows from "
+              "positions U[0,4096)")
+    kernel = "split_rmsnorm_rope_kernel"
+    T, HQ, HKV, HD = 256, 32, 8, 128
+    # qkv in + q/k/v out (fp32) + q/k weights + sin/cos rows
+    algo_bytes = (T * (HQ + 2 * HKV) * HD * 4 * 2 + 2 * HD * 4 + 2 * T * HD * 4)
+
+    def __init__(self):
+        from oracle import rope as orp
+        g = torch.Generator().manual_seed(0)
+        hid = (self.HQ + 2 * self.HKV) * self.HD
+        self.qkv = _randn((self.T, hid), g, torch.float32)
+        self.qw = _randn((self.HD,), g, torch.float32, 0.1, 1.0)
+        self.kw = _randn((self.HD,), g, torch.float32, 0.1, 1.0)
+        pos = torch.randint(0, 4096, (self.T,), generator=g)
+        self.cos, self.sin = orp.neox_cos_sin(pos, orp.inv_freq_table(self.HD, 1e6))
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        qw, kw = self.qw.to(dev), self.kw.to(dev)
+        qh, kvh = self.HQ * self.HD, self.HKV * self.HD
+        out = []
+        for _ in range(n):
+            qkv, sin, cos = self.qkv.to(dev), self.sin.to(dev), self.cos.to(dev)
+            q = torch.empty(self.T, qh, device=dev)
+            k = torch.empty(self.T, kvh, device=dev)
+            v = torch.empty(self.T, kvh, device=dev)
+
+            def run(qkv=qkv, sin=sin, cos=cos, q=q, k=k, v=v):
+                _ok(lib.xk_split_rmsnorm_rope(
+                    qkv.data_ptr(), qkv.stride(0), self.T, sin.data_ptr(),
+                    cos.data_ptr(), self.HD, None, _lib.XK_I64, None,
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), qw.data_ptr(), None,
+                    kw.data_ptr(), None, _lib.XK_F32, qh, kvh, self.HD, 1e-6,
+                    _lib.XK_F32, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import rope as orp
+        a = (self.qkv, self.sin, self.cos, self.qw, self.kw,
+             self.HQ * self.HD, self.HKV * self.HD, self.HD, 1e-6)
+        return (lambda: orp.split_rmsnorm_rope(*a),
+                "full config 1 (256 tokens), fp32", 1.0)
+
+
+CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase)}
 HEADLINE = "layer_norm_fwd"
 
 
 # ---------------------------------------------------------------------------
 # Timing
 # ---------------------------------------------------------------------------
-def time_gpu(case: Case, dev, steps: int, warmup: int):
+def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
     per_set = max(case.algo_bytes, 1)
-    nsets = max(2, min(16, -(-ROTATE_BYTES // per_set)))
+    nsets = max(2, min(MAX_SETS, -(-ROTATE_BYTES // per_set)))
     runs = case.sets(dev, nsets)
-    for i in range(warmup):
-        runs[i % nsets]()
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(warmup):
+            runs[i % nsets]()
+    torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
-    # Whole-region time (ms_per_step) ...
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    t0.record()
-    for i in range(steps):
-        runs[i % nsets]()
-    t1.record()
-    torch.cuda.synchronize()
-    ms_per_step = t0.elapsed_time(t1) / steps
-    # ... and per-launch event pairs for the kernel's own duration.  The
-    # kernels run on torch's current stream, where these events are recorded.
-    evs = [(torch.cuda.Event(enable_timing=True),
-            torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for i, (a, b) in enumerate(evs):
-        a.record()
-        runs[i % nsets]()
-        b.record()
-    torch.cuda.synchronize()
-    launch_ms = [a.elapsed_time(b) for a, b in evs]
+    if eager:
+        t0.record()
+        for i in range(steps):
+            runs[i % nsets]()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+    else:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(steps):
+                runs[i % nsets]()
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = []
+        for _ in range(3):
+            t0.record()
+            graph.replay()
+            t1.record()
+            torch.cuda.synchronize()
+            reps.append(t0.elapsed_time(t1) / steps)
+        ms = statistics.median(reps)
+        del graph
     del runs
+    torch.cuda.synchronize()
     torch.cuda.empty_cache()
-    return ms_per_step, statistics.mean(launch_ms), statistics.median(launch_ms)
+    return ms
 
 
 def time_cpu(case: Case):
@@ -196,10 +258,9 @@ def time_cpu(case: Case):
         t = time.perf_counter()
         run()
         ts.append(time.perf_counter() - t)
-        if time.perf_counter() > budget_end and len(ts) >= 1:
+        if time.perf_counter() > budget_end:
             break
-    sec = statistics.median(ts) * scale
-    return sec, sample, len(ts)
+    return statistics.median(ts) * scale, sample, len(ts)
 
 
 def main():
@@ -209,10 +270,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--op", default=None, help="time only this op")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches instead of a graph replay")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
-              "the ops are per-rank kernels with no collectives, so run it "
+              "these ops are per-rank kernels with no collectives, so run it "
               "with --gpus 1", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
@@ -224,22 +287,20 @@ def main():
     ops = {}
     for name in names:
         case = CASES[name]()
-        ms, launch_mean, launch_med = time_gpu(case, dev, args.steps, args.warmup)
+        ms = time_gpu(case, dev, args.steps, args.warmup, args.eager)
         gbs = case.algo_bytes / (ms * 1e-3) / 1e9
-        kgbs = case.algo_bytes / (launch_mean * 1e-3) / 1e9
         ops[name] = {
             "config": case.config,
+            "kernel": case.kernel,
             "us_per_call": round(ms * 1e3, 2),
-            "kernel_us_mean": round(launch_mean * 1e3, 2),
-            "kernel_us_median": round(launch_med * 1e3, 2),
             "algo_bytes": case.algo_bytes,
             "GB/s": round(gbs, 1),
-            "roofline": {"bound": "hbm", "achieved": round(kgbs, 1),
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1),
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": round(kgbs / HBM_PEAK_GBS, 4)},
+                         "frac": round(gbs / HBM_PEAK_GBS, 4)},
         }
-        print(f"[bench] {name}: {ms*1e3:.1f} us/call, {gbs:.0f} GB/s", file=sys.stderr,
-              flush=True)
+        print(f"[bench] {name}: {ms*1e3:.2f} us/call, {gbs:.0f} GB/s "
+              f"({gbs / HBM_PEAK_GBS:.1%} of peak)", file=sys.stderr, flush=True)
     head = ops[headline]
     case = CASES[headline]()
     cpu = None
@@ -248,7 +309,8 @@ def main():
         cpu = {"value": round(case.algo_bytes / sec / 1e9, 2), "unit": "GB/s",
                "cores": CPU_THREADS, "kind": "port",
                "sample": f"{sample}; median of {nrun} runs, {sec*1e3:.1f} ms/call"}
-        print(f"[bench] cpu baseline {headline}: {sec*1e3:.1f} ms/call", file=sys.stderr)
+        print(f"[bench] cpu baseline {headline}: {sec*1e3:.1f} ms/call",
+              file=sys.stderr, flush=True)
     line = {
         "metric": "achieved HBM GB/s (% of peak) per op; chunked GDN prefill tokens/s",
         "value": head["GB/s"],

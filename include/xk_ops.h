@@ -87,6 +87,33 @@ int xk_l2norm_last_dim(const void* x, void* y, int64_t rows, int64_t cols,
                        float eps, xk_dtype dtype, xk_dtype out_dtype,
                        void* stream);
 
+/* ------------------------------------------------------------------------
+ * a1. Split a packed [T, q_hidden + 2*kv_hidden] row into q, k, v; per-head
+ * RMSNorm of q and k (x * 1/sqrt(mean(x^2)+eps) * w (+ b)) followed by neox
+ * rotate-half RoPE over the whole head; v copied through.
+ * Replaces xllm::kernel::npu::npu_split_rmsnorm_rope
+ *   (triton_npu/torch_api/triton_ops_api.h:186-198,
+ *    npu_triton_split_rmsnorm_rope.cpp:56-144).
+ *   cos/sin : [T, head_dim] rows (stride_sc_row), dtype aux_dtype; or, when
+ *     `positions` (int32/int64 [T]) is given, computed in registers as
+ *     cos/sin(pos * inv_freq[d mod head_dim/2]) from the fp32 table
+ *     inv_freq[head_dim/2] (sin/cos pointers then ignored).
+ *   q_weight, k_weight (+ optional biases): [head_dim], dtype aux_dtype.
+ *   q_out [T, q_hidden], k_out / v_out [T, kv_hidden], dtype `dtype`.
+ *   aux_dtype is `dtype` or XK_F32; head_dim is 64, 128 or 256.
+ */
+int xk_split_rmsnorm_rope(const void* qkv, int64_t stride_qkv_row,
+                          int64_t num_tokens, const void* sin,
+                          const void* cos, int64_t stride_sc_row,
+                          const void* positions, xk_dtype pos_dtype,
+                          const float* inv_freq, void* q_out, void* k_out,
+                          void* v_out, const void* q_weight,
+                          const void* q_bias, const void* k_weight,
+                          const void* k_bias, xk_dtype aux_dtype,
+                          int64_t q_hidden, int64_t kv_hidden,
+                          int64_t head_dim, float eps, xk_dtype dtype,
+                          void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -40,6 +40,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "xk_gemma_rms_norm": ([P, I64, P, I64, P, P, I64, I64, F32, INT, INT, P],
                           INT),
     "xk_l2norm_last_dim": ([P, P, I64, I64, F32, INT, INT, P], INT),
+    "xk_split_rmsnorm_rope": (
+        [P, I64, I64, P, P, I64, P, INT, P, P, P, P, P, P, P, P, INT, I64, I64,
+         I64, F32, INT, P], INT),
 }
 
 _LIB = None

@@ -1,0 +1,264 @@
+// Fused split + per-head RMSNorm + neox RoPE for gfx950
+// (xllm::kernel::npu::npu_split_rmsnorm_rope).
+//
+// Semantics follow the reference CPU golden
+// (triton_npu/test/triton_split_rmsnorm_rope_test.cpp:88-136) and the
+// Python reference (triton_npu/triton_src/test_split_rmsnorm_rope.py:
+// 277-356): from a packed row [q_hidden | kv_hidden | kv_hidden]
+//   q, k : per head of `head_dim`, n = x * 1/sqrt(mean(x^2) + eps) * w (+ b)
+//          then out = n * cos + rotate_half(n) * sin,
+//          rotate_half(n) = cat(-n[half:], n[:half])
+//   v    : copied through.
+// cos/sin are either per-token rows [T, head_dim] (the reference's
+// interface) or computed in registers from integer positions and an fp32
+// inverse-frequency table (neox layout: cos[d] = cos[d + half]).
+//
+// Design: one team of HALF/VEC lanes per (token, head).  Lane l holds the
+// VEC-element slices [l*VEC, l*VEC+VEC) and [half + l*VEC, ...) of the
+// head, so the rotate-half pairs (d, d + half) sit in the same lane and the
+// rotation needs no data exchange.  The head's sum of squares is a shuffle
+// reduction over the team; every global access is a 16-byte vector.
+#include <type_traits>
+
+#include "xk_common.h"
+
+namespace xk {
+namespace {
+
+struct RopeParams {
+  const void* qkv;
+  int64_t stride_row;  // elements between tokens of qkv
+  int64_t T;
+  const void* sin;
+  const void* cos;
+  int64_t stride_sc;
+  const void* pos;
+  int pos_is_i64;
+  const float* inv_freq;
+  void* q;
+  void* k;
+  void* v;
+  const void* qw;
+  const void* qb;
+  const void* kw;
+  const void* kb;
+  int hq, hkv;  // heads
+  int64_t q_hidden, kv_hidden;
+  float eps;
+};
+
+template <typename T, int N>
+__device__ __forceinline__ void ld_f32(const T* p, float (&o)[N]) {
+  const Vec<T, N> v = *reinterpret_cast<const Vec<T, N>*>(p);
+#pragma unroll
+  for (int i = 0; i < N; ++i) o[i] = to_f32(v.v[i]);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void st_f32(T* p, const float (&in)[N]) {
+  Vec<T, N> v;
+#pragma unroll
+  for (int i = 0; i < N; ++i) v.v[i] = from_f32<T>(in[i]);
+  *reinterpret_cast<Vec<T, N>*>(p) = v;
+}
+
+template <typename T, typename A, int HD>
+__global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
+  constexpr int kHalf = HD / 2;
+  constexpr int kVec = (16 / sizeof(T)) < kHalf ? (16 / sizeof(T)) : kHalf;
+  constexpr int kTeam = kHalf / kVec;
+  static_assert(kTeam >= 1 && kTeam <= kWave, "team must fit a wave");
+  constexpr int kTeams = 256 / kTeam;
+
+  const int team = threadIdx.x / kTeam;
+  const int lane = threadIdx.x % kTeam;
+  const int heads = p.hq + 2 * p.hkv;
+  const int64_t slot = static_cast<int64_t>(blockIdx.x) * kTeams + team;
+  if (slot >= p.T * heads) return;  // whole team exits together
+  const int64_t tok = slot / heads;
+  const int h = static_cast<int>(slot - tok * heads);
+  const int d0 = lane * kVec;
+
+  const T* row = reinterpret_cast<const T*>(p.qkv) + tok * p.stride_row;
+  if (h >= p.hq + p.hkv) {  // v: copy through
+    const int hv = h - p.hq - p.hkv;
+    const T* src = row + p.q_hidden + p.kv_hidden + static_cast<int64_t>(hv) * HD;
+    T* dst = reinterpret_cast<T*>(p.v) + tok * p.kv_hidden + static_cast<int64_t>(hv) * HD;
+    using VT = Vec<T, kVec>;
+    *reinterpret_cast<VT*>(dst + d0) = *reinterpret_cast<const VT*>(src + d0);
+    *reinterpret_cast<VT*>(dst + kHalf + d0) =
+        *reinterpret_cast<const VT*>(src + kHalf + d0);
+    return;
+  }
+  const bool is_q = h < p.hq;
+  const int hh = is_q ? h : h - p.hq;
+  const T* src = row + (is_q ? 0 : p.q_hidden) + static_cast<int64_t>(hh) * HD;
+  T* dst = reinterpret_cast<T*>(is_q ? p.q : p.k) +
+           tok * (is_q ? p.q_hidden : p.kv_hidden) + static_cast<int64_t>(hh) * HD;
+  const A* w = reinterpret_cast<const A*>(is_q ? p.qw : p.kw);
+  const A* b = reinterpret_cast<const A*>(is_q ? p.qb : p.kb);
+
+  float x1[kVec], x2[kVec];
+  ld_f32<T, kVec>(src + d0, x1);
+  ld_f32<T, kVec>(src + kHalf + d0, x2);
+  float ss = 0.f;
+#pragma unroll
+  for (int u = 0; u < kVec; ++u) ss = fmaf(x1[u], x1[u], fmaf(x2[u], x2[u], ss));
+  ss = group_sum<kTeam>(ss);
+  const float r = 1.0f / sqrtf(ss * (1.0f / HD) + p.eps);
+
+  float w1[kVec], w2[kVec];
+  ld_f32<A, kVec>(w + d0, w1);
+  ld_f32<A, kVec>(w + kHalf + d0, w2);
+  float n1[kVec], n2[kVec];
+#pragma unroll
+  for (int u = 0; u < kVec; ++u) {
+    n1[u] = x1[u] * r * w1[u];
+    n2[u] = x2[u] * r * w2[u];
+  }
+  if (b) {
+    float b1[kVec], b2[kVec];
+    ld_f32<A, kVec>(b + d0, b1);
+    ld_f32<A, kVec>(b + kHalf + d0, b2);
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      n1[u] += b1[u];
+      n2[u] += b2[u];
+    }
+  }
+
+  float c1[kVec], c2[kVec], s1[kVec], s2[kVec];
+  if (p.pos) {
+    const float pos = p.pos_is_i64
+                          ? static_cast<float>(reinterpret_cast<const int64_t*>(p.pos)[tok])
+                          : static_cast<float>(reinterpret_cast<const int32_t*>(p.pos)[tok]);
+    float f[kVec];
+    ld_f32<float, kVec>(p.inv_freq + d0, f);
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      sincosf(pos * f[u], &s1[u], &c1[u]);
+      s2[u] = s1[u];
+      c2[u] = c1[u];
+    }
+  } else {
+    const A* cs = reinterpret_cast<const A*>(p.cos) + tok * p.stride_sc;
+    const A* sn = reinterpret_cast<const A*>(p.sin) + tok * p.stride_sc;
+    ld_f32<A, kVec>(cs + d0, c1);
+    ld_f32<A, kVec>(cs + kHalf + d0, c2);
+    ld_f32<A, kVec>(sn + d0, s1);
+    ld_f32<A, kVec>(sn + kHalf + d0, s2);
+  }
+  float o1[kVec], o2[kVec];
+#pragma unroll
+  for (int u = 0; u < kVec; ++u) {
+    o1[u] = n1[u] * c1[u] - n2[u] * s1[u];
+    o2[u] = n2[u] * c2[u] + n1[u] * s2[u];
+  }
+  st_f32<T, kVec>(dst + d0, o1);
+  st_f32<T, kVec>(dst + kHalf + d0, o2);
+}
+
+template <typename T, typename A, int HD>
+int launch_rope(const RopeParams& p, hipStream_t s) {
+  constexpr int kHalf = HD / 2;
+  constexpr int kVec = (16 / sizeof(T)) < kHalf ? (16 / sizeof(T)) : kHalf;
+  constexpr int kTeams = 256 / (kHalf / kVec);
+  const int64_t slots = p.T * (p.hq + 2 * p.hkv);
+  hipLaunchKernelGGL((split_rmsnorm_rope_kernel<T, A, HD>), dim3(cdiv(slots, kTeams)),
+                     dim3(256), 0, s, p);
+  return launch_status();
+}
+
+template <typename T, typename A>
+int dispatch_hd(const RopeParams& p, int64_t hd, hipStream_t s) {
+  switch (hd) {
+    case 64: return launch_rope<T, A, 64>(p, s);
+    case 128: return launch_rope<T, A, 128>(p, s);
+    case 256: return launch_rope<T, A, 256>(p, s);
+    default: return XK_ERR_UNSUPPORTED;
+  }
+}
+
+template <typename T>
+int dispatch_aux(const RopeParams& p, int64_t hd, xk_dtype dt, xk_dtype aux,
+                 hipStream_t s) {
+  if (aux == dt) return dispatch_hd<T, T>(p, hd, s);
+  if (aux == XK_F32) return dispatch_hd<T, float>(p, hd, s);
+  return XK_ERR_UNSUPPORTED;
+}
+
+}  // namespace
+}  // namespace xk
+
+using namespace xk;
+
+extern "C" int xk_split_rmsnorm_rope(
+    const void* qkv, int64_t stride_qkv_row, int64_t num_tokens,
+    const void* sin, const void* cos, int64_t stride_sc_row,
+    const void* positions, xk_dtype pos_dtype, const float* inv_freq,
+    void* q_out, void* k_out, void* v_out, const void* q_weight,
+    const void* q_bias, const void* k_weight, const void* k_bias,
+    xk_dtype aux_dtype, int64_t q_hidden, int64_t kv_hidden, int64_t head_dim,
+    float eps, xk_dtype dtype, void* stream) {
+  if (num_tokens < 0 || head_dim <= 0 || (head_dim & (head_dim - 1)) != 0 ||
+      q_hidden <= 0 || kv_hidden <= 0 || q_hidden % head_dim != 0 ||
+      kv_hidden % head_dim != 0 || stride_qkv_row < q_hidden + 2 * kv_hidden)
+    return XK_ERR_INVALID;
+  if (!is_float_dtype(dtype) || !is_float_dtype(aux_dtype))
+    return XK_ERR_UNSUPPORTED;
+  if (positions && pos_dtype != XK_I32 && pos_dtype != XK_I64)
+    return XK_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return XK_OK;
+  if (!qkv || !q_out || !k_out || !v_out || !q_weight || !k_weight)
+    return XK_ERR_INVALID;
+  if (positions ? !inv_freq : (!sin || !cos || stride_sc_row < head_dim))
+    return XK_ERR_INVALID;
+  const int vec_bytes = 16;
+  const int eb = elem_bytes(dtype);
+  // Every row, head and half-head slice must start on a vector boundary.
+  if ((stride_qkv_row * eb) % vec_bytes || !aligned(qkv, vec_bytes) ||
+      !aligned(q_out, vec_bytes) || !aligned(k_out, vec_bytes) ||
+      !aligned(v_out, vec_bytes))
+    return XK_ERR_INVALID;
+  // Aux vectors (weights, bias, sin/cos, inv_freq) are loaded with the
+  // same element count as x: 16 bytes of x may mean 32 bytes of fp32 aux.
+  const int aux_bytes = elem_bytes(aux_dtype) * (vec_bytes / eb);
+  if (!aligned(q_weight, aux_bytes) || !aligned(k_weight, aux_bytes) ||
+      (q_bias && !aligned(q_bias, aux_bytes)) ||
+      (k_bias && !aligned(k_bias, aux_bytes)))
+    return XK_ERR_INVALID;
+  if (positions && !aligned(inv_freq, 4 * (vec_bytes / eb)))
+    return XK_ERR_INVALID;
+  if (!positions && ((stride_sc_row * elem_bytes(aux_dtype)) % aux_bytes ||
+                     !aligned(sin, aux_bytes) || !aligned(cos, aux_bytes)))
+    return XK_ERR_INVALID;
+  RopeParams p{};
+  p.qkv = qkv;
+  p.stride_row = stride_qkv_row;
+  p.T = num_tokens;
+  p.sin = sin;
+  p.cos = cos;
+  p.stride_sc = stride_sc_row;
+  p.pos = positions;
+  p.pos_is_i64 = pos_dtype == XK_I64;
+  p.inv_freq = inv_freq;
+  p.q = q_out;
+  p.k = k_out;
+  p.v = v_out;
+  p.qw = q_weight;
+  p.qb = q_bias;
+  p.kw = k_weight;
+  p.kb = k_bias;
+  p.hq = static_cast<int>(q_hidden / head_dim);
+  p.hkv = static_cast<int>(kv_hidden / head_dim);
+  p.q_hidden = q_hidden;
+  p.kv_hidden = kv_hidden;
+  p.eps = eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case XK_F32: return dispatch_aux<float>(p, head_dim, dtype, aux_dtype, s);
+    case XK_BF16: return dispatch_aux<bf16>(p, head_dim, dtype, aux_dtype, s);
+    case XK_F16: return dispatch_aux<f16>(p, head_dim, dtype, aux_dtype, s);
+    default: return XK_ERR_UNSUPPORTED;
+  }
+}

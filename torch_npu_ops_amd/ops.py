@@ -127,6 +127,74 @@ def npu_gemma_rms_norm(x: torch.Tensor, gamma: torch.Tensor, epsilon: float):
     return y.reshape(x.shape), rstd
 
 
+def npu_split_rmsnorm_rope(input: torch.Tensor, sin: Optional[torch.Tensor],
+                           cos: Optional[torch.Tensor], q_weight: torch.Tensor,
+                           k_weight: torch.Tensor, q_hidden_size: int,
+                           kv_hidden_size: int, head_dim: int, eps: float,
+                           q_bias: Optional[torch.Tensor] = None,
+                           k_bias: Optional[torch.Tensor] = None,
+                           bias: bool = False,
+                           positions: Optional[torch.Tensor] = None,
+                           inv_freq: Optional[torch.Tensor] = None):
+    """Split + q/k RMSNorm + neox RoPE; returns (q, k, v).
+
+    Mirrors npu_split_rmsnorm_rope
+    (triton_npu/torch_api/npu_triton_split_rmsnorm_rope.cpp:56-144),
+    including its shape checks; biases are used only when ``bias`` is set
+    and both tensors are given (:109-118).  With ``positions`` (and an fp32
+    ``inv_freq`` [head_dim/2]) cos/sin are computed in the kernel and the
+    sin/cos arguments may be None.  The reference's launch-shape constraint
+    (32 % n_kv_heads == 0, :94-96) does not apply to this kernel.
+    """
+    if input.dim() != 2:
+        raise ValueError("split_rmsnorm_rope input must be a 2D tensor")
+    if head_dim <= 0 or head_dim & (head_dim - 1):
+        raise ValueError("split_rmsnorm_rope head_dim must be a power of two")
+    if q_hidden_size % kv_hidden_size:
+        raise ValueError("split_rmsnorm_rope q_hidden_size must be divisible "
+                         "by kv_hidden_size")
+    if kv_hidden_size % head_dim:
+        raise ValueError("split_rmsnorm_rope kv_hidden_size must be divisible "
+                         "by head_dim")
+    if input.size(1) != q_hidden_size + 2 * kv_hidden_size:
+        raise ValueError("split_rmsnorm_rope input hidden size mismatch")
+    if q_weight.numel() != head_dim or k_weight.numel() != head_dim:
+        raise ValueError("split_rmsnorm_rope q/k weight shape mismatch")
+    T = input.size(0)
+    x = input if input.stride(1) == 1 else input.contiguous()
+    aux = q_weight.dtype
+    qw, kw = q_weight.contiguous(), k_weight.contiguous().to(aux)
+    qb = kb = None
+    if bias and q_bias is not None and k_bias is not None:
+        qb, kb = q_bias.contiguous().to(aux), k_bias.contiguous().to(aux)
+    pos_ptr, pos_dt, inv_ptr = None, _lib.XK_I64, None
+    sin_ptr = cos_ptr = None
+    stride_sc = head_dim
+    if positions is not None:
+        if inv_freq is None or inv_freq.numel() != head_dim // 2:
+            raise ValueError("positions mode needs inv_freq of head_dim/2 fp32")
+        positions = positions.contiguous()
+        inv_freq = inv_freq.to(torch.float32).contiguous()
+        pos_ptr, pos_dt, inv_ptr = positions.data_ptr(), xk_dtype(positions), inv_freq.data_ptr()
+    else:
+        if (sin.dim() != 2 or cos.dim() != 2 or sin.size(0) != T or cos.size(0) != T
+                or sin.size(1) != head_dim or cos.size(1) != head_dim):
+            raise ValueError("split_rmsnorm_rope sin/cos shape mismatch")
+        sin = sin.to(aux).contiguous()
+        cos = cos.to(aux).contiguous()
+        sin_ptr, cos_ptr = sin.data_ptr(), cos.data_ptr()
+    q = torch.empty((T, q_hidden_size), dtype=input.dtype, device=input.device)
+    k = torch.empty((T, kv_hidden_size), dtype=input.dtype, device=input.device)
+    v = torch.empty((T, kv_hidden_size), dtype=input.dtype, device=input.device)
+    st = lib().xk_split_rmsnorm_rope(
+        x.data_ptr(), x.stride(0), T, sin_ptr, cos_ptr, stride_sc, pos_ptr,
+        pos_dt, inv_ptr, q.data_ptr(), k.data_ptr(), v.data_ptr(), qw.data_ptr(),
+        _ptr(qb), kw.data_ptr(), _ptr(kb), xk_dtype(qw), q_hidden_size,
+        kv_hidden_size, head_dim, float(eps), xk_dtype(x), _stream(input))
+    check(st, "xk_split_rmsnorm_rope")
+    return q, k, v
+
+
 def npu_l2norm_last_dim(x: torch.Tensor, eps: float = 1e-6,
                         output_dtype: Optional[torch.dtype] = None):
     """x * rsqrt(sum(x^2) + eps) over the last dim.
