@@ -199,7 +199,112 @@ class RopeCase(Case):
                 "full config 1 (256 tokens), fp32", 1.0)
 
 
-CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase)}
+def varlen_lengths(n, total, lo, hi, gen):
+    """n lengths ~ U{lo..hi}, repaired at seeded positions to sum to total."""
+    lens = torch.randint(lo, hi + 1, (n,), generator=gen)
+    diff = total - int(lens.sum())
+    i = 0
+    while diff != 0:
+        j = i % n
+        step = max(-(int(lens[j]) - lo), min(hi - int(lens[j]), diff))
+        lens[j] += step
+        diff -= step
+        i += 1
+    return lens
+
+
+class ConvPrefillCase(Case):
+    name = "causal_conv1d_prefill"
+    config = ("config 3a: causal_conv1d varlen prefill bf16, 8 sequences "
+              "(lengths U[512,3584], 16384 tokens), dim 8192, width 4, SiLU, "
+              "w~N(0,0.5), zero initial state")
+    kernel = "conv1d_varlen_kernel"
+    T, D, W, NSEQ = 16384, 8192, 4, 8
+    # x + y (bf16) + weights + state read/write
+    algo_bytes = T * D * 2 * 2 + D * W * 2 + NSEQ * D * (W - 1) * 2 * 2
+
+    def __init__(self):
+        g = torch.Generator().manual_seed(0)
+        lens = varlen_lengths(self.NSEQ, self.T, 512, 3584, g)
+        self.qsl = torch.zeros(self.NSEQ + 1, dtype=torch.int32)
+        self.qsl[1:] = torch.cumsum(lens, 0)
+        self.mql = int(lens.max())
+        self.x = _randn((self.T, self.D), g, torch.bfloat16)
+        self.w = _randn((self.D, self.W), g, torch.bfloat16, 0.5)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        w, qsl = self.w.to(dev), self.qsl.to(dev)
+        out = []
+        for _ in range(n):
+            x = self.x.to(dev)
+            y = torch.empty_like(x)
+            st = torch.zeros(self.NSEQ, self.D, self.W - 1, dtype=torch.bfloat16,
+                             device=dev)
+
+            def run(x=x, y=y, st=st):
+                _ok(lib.xk_causal_conv1d_varlen(
+                    x.data_ptr(), self.D, self.T, y.data_ptr(), self.D,
+                    st.data_ptr(), st.stride(0), st.stride(1), st.stride(2),
+                    self.NSEQ, self.W - 1, w.data_ptr(), self.W, 1, None,
+                    _lib.XK_BF16, qsl.data_ptr(), self.NSEQ, None, 0, 0, None,
+                    None, None, self.D, self.W, self.mql, 0, 1, -1,
+                    _lib.XK_BF16, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import conv1d as oc
+        st = torch.zeros(self.NSEQ, self.D, self.W - 1, dtype=torch.bfloat16)
+        a = (self.x, st, self.w, None, True, None, self.qsl, self.mql)
+        return (lambda: oc.causal_conv1d_update_v2(*a),
+                "full config 3a (16384 tokens x 8192), per-sequence F.conv1d fp32", 1.0)
+
+
+class ConvDecodeCase(Case):
+    name = "causal_conv1d_update"
+    config = ("config 3b: causal_conv1d decode update bf16, batch 256 x dim 8192, "
+              "conv_state [256,8192,3] ~N(0,1), width 4, SiLU, indices arange")
+    kernel = "conv1d_update_w4_kernel"
+    B, D, W = 256, 8192, 4
+    algo_bytes = B * D * 2 * 2 + B * D * (W - 1) * 2 * 2 + D * W * 2
+
+    def __init__(self):
+        g = torch.Generator().manual_seed(0)
+        self.x = _randn((self.B, self.D), g, torch.bfloat16)
+        self.state = _randn((self.B, self.D, self.W - 1), g, torch.bfloat16)
+        self.w = _randn((self.D, self.W), g, torch.bfloat16, 0.5)
+        self.idx = torch.arange(self.B, dtype=torch.int32)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        w, idx = self.w.to(dev), self.idx.to(dev)
+        out = []
+        for _ in range(n):
+            x, st = self.x.to(dev), self.state.to(dev)
+            y = torch.empty_like(x)
+
+            def run(x=x, y=y, st=st):
+                _ok(lib.xk_causal_conv1d_update(
+                    x.data_ptr(), self.D, 1, 1, st.data_ptr(), st.stride(0),
+                    st.stride(1), st.stride(2), w.data_ptr(), self.W, 1, None,
+                    _lib.XK_BF16, idx.data_ptr(), -1, self.B, y.data_ptr(),
+                    self.D, 1, 1, self.B, self.D, 1, self.W, self.W - 1, 1,
+                    _lib.XK_BF16, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import conv1d as oc
+        a = (self.x, self.state, self.w, None, True, self.idx)
+        return (lambda: oc.causal_conv1d_update(*a),
+                "full config 3b (256 x 8192), fp32", 1.0)
+
+
+CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
+                             ConvDecodeCase)}
 HEADLINE = "layer_norm_fwd"
 
 

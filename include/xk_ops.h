@@ -114,6 +114,62 @@ int xk_split_rmsnorm_rope(const void* qkv, int64_t stride_qkv_row,
                           int64_t head_dim, float eps, xk_dtype dtype,
                           void* stream);
 
+/* ------------------------------------------------------------------------
+ * a4. Depthwise causal conv1d state update (decode / short MTP windows).
+ * Replaces xllm::kernel::npu::npu_causal_conv1d_update
+ *   (triton_npu/torch_api/triton_ops_api.h:147-160,
+ *    npu_triton_causal_conv1d_update.cpp:22-138).
+ *   x, out : [batch, dim, seqlen] (strides); conv_state : [lines, dim,
+ *   state_len] (strides), updated in place to the last state_len entries of
+ *   cat(state, x); weight [dim, width] (strides), bias [dim] or NULL, both
+ *   dtype wdtype (x's dtype or fp32).  Slot b = conv_state_indices[b] (or b
+ *   when NULL); slots equal to pad_slot_id or outside [0, num_cache_lines)
+ *   are skipped (no output, no state write).  activation != 0 applies SiLU.
+ *   state_len >= width - 1.
+ */
+int xk_causal_conv1d_update(
+    const void* x, int64_t stride_x_batch, int64_t stride_x_dim,
+    int64_t stride_x_token, void* conv_state, int64_t stride_state_line,
+    int64_t stride_state_dim, int64_t stride_state_token,
+    const void* weight, int64_t stride_w_dim, int64_t stride_w_tap,
+    const void* bias, xk_dtype wdtype, const int32_t* conv_state_indices,
+    int32_t pad_slot_id, int64_t num_cache_lines, void* out,
+    int64_t stride_o_batch, int64_t stride_o_dim, int64_t stride_o_token,
+    int64_t batch, int64_t dim, int64_t seqlen, int64_t width,
+    int64_t state_len, int activation, xk_dtype dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * a5. Varlen depthwise causal conv1d with conv-state slots (prefill, APC,
+ * speculative decoding).
+ * Replaces xllm::kernel::npu::npu_causal_conv1d_update_v2
+ *   (triton_npu/torch_api/triton_ops_api.h:162-176,
+ *    npu_triton_causal_conv1d_update_v2.cpp:99-239).
+ *   x, out : [num_tokens, dim] token-major (token strides); sequence s is
+ *     rows [query_start_loc[s], query_start_loc[s+1]), s < batch.
+ *   conv_state : [num_cache_lines, dim, state_len] (strides).
+ *   slot_table : NULL (slot = s), 1-D [batch] (slot_table_2d = 0) or 2-D
+ *     [batch, slot_table_stride] whose columns initial_state_idx[s] /
+ *     last_state_idx[s] (NULL = column 0) give the input / output slot.
+ *   num_accepted_tokens : NULL, or [batch] for speculative decoding.
+ *   state_rule 0 reproduces the reference's final-state rule
+ *     (state_len_run = eff - (max_query_len - len)); 1 keeps the last
+ *     eff = width-1 (+ max_query_len-1 with spec decoding) inputs of every
+ *     sequence.  Sequences whose input slot is pad_slot_id are skipped.
+ *   width in [1, 8]; launches two kernels (conv, then final states).
+ */
+int xk_causal_conv1d_varlen(
+    const void* x, int64_t stride_x_token, int64_t num_tokens, void* out,
+    int64_t stride_o_token, void* conv_state, int64_t stride_state_line,
+    int64_t stride_state_dim, int64_t stride_state_token,
+    int64_t num_cache_lines, int64_t state_len, const void* weight,
+    int64_t stride_w_dim, int64_t stride_w_tap, const void* bias,
+    xk_dtype wdtype, const int32_t* query_start_loc, int64_t batch,
+    const int32_t* slot_table, int64_t slot_table_stride, int slot_table_2d,
+    const int32_t* initial_state_idx, const int32_t* last_state_idx,
+    const int32_t* num_accepted_tokens, int64_t dim, int64_t width,
+    int64_t max_query_len, int state_rule, int activation,
+    int32_t pad_slot_id, xk_dtype dtype, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

@@ -43,6 +43,13 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "xk_split_rmsnorm_rope": (
         [P, I64, I64, P, P, I64, P, INT, P, P, P, P, P, P, P, P, INT, I64, I64,
          I64, F32, INT, P], INT),
+    "xk_causal_conv1d_update": (
+        [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, P, INT, P, I32, I64,
+         P, I64, I64, I64, I64, I64, I64, I64, I64, INT, INT, P], INT),
+    "xk_causal_conv1d_varlen": (
+        [P, I64, I64, P, I64, P, I64, I64, I64, I64, I64, P, I64, I64, P, INT,
+         P, I64, P, I64, INT, P, P, P, I64, I64, I64, INT, INT, I32, INT, P],
+        INT),
 }
 
 _LIB = None

@@ -1,0 +1,495 @@
+// Depthwise causal conv1d for gfx950: single-step state update (decode)
+// and varlen prefill with conv-state slots.
+//
+// Update (xllm::kernel::npu::npu_causal_conv1d_update) follows
+// causal_conv1d_update_ref (triton_npu/triton_src/test_causal_conv1d_update.py:
+// 1158-1210, no cache_seqlens): per channel
+//   xs   = cat(state[0:S], x[0:T])                 (S = state_len >= W-1)
+//   out_t = act(bias + sum_j w[j] * xs[S-W+1+t+j])
+//   state <- xs[T:T+S]
+// with the slot taken from conv_state_indices and pad_slot_id slots skipped
+// (test_causal_conv1d_update.py:886-939).
+//
+// Varlen (npu_causal_conv1d_update_v2) follows the CPU golden
+// causal_conv1d_update_ref_v2 (triton_npu/test/triton_causal_conv1d_update_v2
+// _test.cpp:59-229) and, for speculative decoding, the kernel
+// test_causal_conv1d_update_v2.py:16-249: per sequence s of
+// query_start_loc, history = state[in_slot][:, off : off+W-1] (zeros if
+// in_slot is out of range), out_t = act(bias + conv(cat(history, x_s))), and
+// the final state rule
+//   state_len_run = eff_state_len - (max_query_len - len)   (reference rule)
+//   len >= state_len_run : state[out_slot][:, :run] = x_s[len-run:]
+//   else                 : state[out_slot][:, :keep] = state[in_slot][:,
+//                          off+shift : off+shift+keep], then x_s
+// where eff_state_len = W-1 (+ max_query_len-1 with spec decoding),
+// off = accepted-1 and shift = 1 with spec decoding, else off = 0 and
+// shift = len.  A "prefill" rule (state_len_run = eff_state_len for every
+// sequence, i.e. the last W-1 inputs) is offered for full-prefill callers.
+//
+// Design: channels are the vector dimension (16-byte accesses along the
+// contiguous channel axis); each lane walks a tile of tokens with the W-1
+// previous inputs in a register window, so every x element is read from
+// HBM once (plus a W-1 token halo per tile, served from L2) and every output
+// written once.  Sequence boundaries inside a tile restart the window from
+// the sequence's state history.  The final-state update is a second, tiny
+// kernel so that no block can overwrite a slot another block still reads
+// as history.
+#include "xk_common.h"
+
+namespace xk {
+namespace {
+
+__device__ __forceinline__ float act(float v, int silu_on) {
+  return silu_on ? silu(v) : v;
+}
+
+// ---------------------------------------------------------------------------
+// Decode update, width 4 / state_len 3 / one token, contiguous layout:
+// x, out [B, D]; state [lines, D, 3]; weight [D, 4].  One lane owns 8
+// channels: 48 contiguous bytes of state (3 x 16 B), 16 B of x, 64 B of
+// weights, and writes 16 B of output plus 48 B of state.
+// ---------------------------------------------------------------------------
+template <typename T, typename WT>
+__global__ void __launch_bounds__(256)
+    conv1d_update_w4_kernel(const T* __restrict__ x, T* __restrict__ out,
+                            T* __restrict__ state, int64_t state_line_stride,
+                            const WT* __restrict__ w, xk_dtype wdt,
+                            const void* __restrict__ bias,
+                            const int32_t* __restrict__ idx, int32_t pad,
+                            int64_t lines, int64_t B, int64_t D, int silu_on) {
+  constexpr int kC = 8;
+  const int64_t b = blockIdx.y;
+  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * kC;
+  if (c0 >= D) return;
+  const int64_t slot = idx ? idx[b] : b;
+  if ((idx && slot == pad) || slot < 0 || slot >= lines) return;
+  T* st = state + slot * state_line_stride + c0 * 3;
+  using V8 = Vec<T, kC>;
+  // 24 state values (channel-major: s[c*3 + k]) as three 8-element vectors.
+  Arr<T, 24> s;
+  *reinterpret_cast<V8*>(&s.v[0]) = reinterpret_cast<const V8*>(st)[0];
+  *reinterpret_cast<V8*>(&s.v[8]) = reinterpret_cast<const V8*>(st)[1];
+  *reinterpret_cast<V8*>(&s.v[16]) = reinterpret_cast<const V8*>(st)[2];
+  const V8 xv = *reinterpret_cast<const V8*>(x + b * D + c0);
+  // The 8 channels' 4 taps are 32 contiguous weights.
+  const Vec<WT, 32> wv = *reinterpret_cast<const Vec<WT, 32>*>(w + c0 * 4);
+  V8 ov;
+  Arr<T, 24> ns;
+#pragma unroll
+  for (int c = 0; c < kC; ++c) {
+    const int64_t ch = c0 + c;
+    const float s0 = to_f32(s.v[c * 3 + 0]);
+    const float s1 = to_f32(s.v[c * 3 + 1]);
+    const float s2 = to_f32(s.v[c * 3 + 2]);
+    const float xc = to_f32(xv.v[c]);
+    float acc = bias ? load_as_f32(bias, ch, wdt) : 0.f;
+    acc = fmaf(s0, to_f32(wv.v[c * 4 + 0]), acc);
+    acc = fmaf(s1, to_f32(wv.v[c * 4 + 1]), acc);
+    acc = fmaf(s2, to_f32(wv.v[c * 4 + 2]), acc);
+    acc = fmaf(xc, to_f32(wv.v[c * 4 + 3]), acc);
+    ov.v[c] = from_f32<T>(act(acc, silu_on));
+    ns.v[c * 3 + 0] = s.v[c * 3 + 1];
+    ns.v[c * 3 + 1] = s.v[c * 3 + 2];
+    ns.v[c * 3 + 2] = xv.v[c];
+  }
+  *reinterpret_cast<V8*>(out + b * D + c0) = ov;
+  reinterpret_cast<V8*>(st)[0] = *reinterpret_cast<const V8*>(&ns.v[0]);
+  reinterpret_cast<V8*>(st)[1] = *reinterpret_cast<const V8*>(&ns.v[8]);
+  reinterpret_cast<V8*>(st)[2] = *reinterpret_cast<const V8*>(&ns.v[16]);
+}
+
+// ---------------------------------------------------------------------------
+// Decode update, any width / state_len / seqlen / strides: one lane per
+// (batch, channel).  All outputs are computed from the old state first, then
+// the state is shifted in ascending order (each new value comes from an
+// equal or later index, so in-place shifting is safe).
+// ---------------------------------------------------------------------------
+struct UpdateParams {
+  const void* x;
+  int64_t sxb, sxd, sxt;
+  void* out;
+  int64_t sob, sod, sot;
+  void* state;
+  int64_t ssl, ssd, sss;
+  const void* w;
+  int64_t swd, sww;
+  xk_dtype wdt;
+  const void* bias;
+  const int32_t* idx;
+  int32_t pad;
+  int64_t lines;
+  int64_t B, D, T, W, S;
+  int silu_on;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) conv1d_update_generic_kernel(UpdateParams p) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (gid >= p.B * p.D) return;
+  const int64_t b = gid / p.D;
+  const int64_t c = gid - b * p.D;
+  const int64_t slot = p.idx ? p.idx[b] : b;
+  if ((p.idx && slot == p.pad) || slot < 0 || slot >= p.lines) return;
+  const T* x = reinterpret_cast<const T*>(p.x) + b * p.sxb + c * p.sxd;
+  T* o = reinterpret_cast<T*>(p.out) + b * p.sob + c * p.sod;
+  T* st = reinterpret_cast<T*>(p.state) + slot * p.ssl + c * p.ssd;
+  auto val = [&](int64_t i) {  // element i of cat(state, x)
+    return i < p.S ? to_f32(st[i * p.sss]) : to_f32(x[(i - p.S) * p.sxt]);
+  };
+  const float bias = p.bias ? load_as_f32(p.bias, c, p.wdt) : 0.f;
+  for (int64_t t = 0; t < p.T; ++t) {
+    float acc = bias;
+    for (int64_t j = 0; j < p.W; ++j)
+      acc = fmaf(val(p.S - p.W + 1 + t + j), load_as_f32(p.w, c * p.swd + j * p.sww, p.wdt), acc);
+    o[t * p.sot] = from_f32<T>(act(acc, p.silu_on));
+  }
+  for (int64_t i = 0; i < p.S; ++i) {
+    const int64_t src = p.T + i;
+    const T v = src < p.S ? st[src * p.sss] : x[(src - p.S) * p.sxt];
+    st[i * p.sss] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Varlen prefill.
+// ---------------------------------------------------------------------------
+struct VarlenParams {
+  const void* x;
+  int64_t sx;  // token stride of x
+  void* out;
+  int64_t so;
+  void* state;
+  int64_t ssl, ssd, sss;  // state strides: line, channel, token
+  int64_t lines;
+  int64_t S;  // state_len (tokens held per channel)
+  const void* w;
+  int64_t swd, sww;
+  xk_dtype wdt;
+  const void* bias;
+  const int32_t* qsl;  // [B + 1]
+  int B;
+  const int32_t* slots;  // NULL: slot = sequence index
+  int64_t slot_stride;   // elements between rows of a 2-D slot table
+  int slot_2d;
+  const int32_t* init_idx;  // column of the input slot (2-D table)
+  const int32_t* last_idx;  // column of the output slot (2-D table)
+  const int32_t* accepted;  // spec decoding: accepted tokens per sequence
+  int64_t D;
+  int W;
+  int64_t num_tokens;  // rows of x (>= qsl[B])
+  int max_query_len;
+  int eff_state_len;
+  int state_rule;  // 0: reference rule, 1: prefill rule
+  int silu_on;
+  int32_t pad;
+};
+
+__device__ __forceinline__ int64_t resolve_slot(const VarlenParams& p, int s,
+                                                const int32_t* col) {
+  if (!p.slots) return s;
+  if (!p.slot_2d) return p.slots[s];
+  const int c = col ? col[s] : 0;
+  return p.slots[static_cast<int64_t>(s) * p.slot_stride + c];
+}
+
+// Index of the sequence holding token t (qsl non-decreasing).
+__device__ __forceinline__ int find_seq(const int32_t* qsl, int B, int64_t t) {
+  int lo = 0, hi = B;  // answer in [0, B)
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (qsl[mid] <= t) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+constexpr int kTileT = 32;  // tokens per lane per tile
+
+template <typename T, int W, int VEC>
+__global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
+  using VT = Vec<T, VEC>;
+  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC;
+  if (c0 >= p.D) return;
+  // Tokens outside [qsl[0], qsl[B]) belong to no sequence and are skipped.
+  const int64_t t0 = max(static_cast<int64_t>(blockIdx.y) * kTileT,
+                         static_cast<int64_t>(p.qsl[0]));
+  const int64_t total = p.qsl[p.B];
+  const int64_t t_end = min(min(static_cast<int64_t>(blockIdx.y + 1) * kTileT, total),
+                            p.num_tokens);
+  if (t0 >= t_end) return;
+
+  float wt[W][VEC], bs[VEC];
+#pragma unroll
+  for (int u = 0; u < VEC; ++u) {
+#pragma unroll
+    for (int j = 0; j < W; ++j)
+      wt[j][u] = load_as_f32(p.w, (c0 + u) * p.swd + j * p.sww, p.wdt);
+    bs[u] = p.bias ? load_as_f32(p.bias, c0 + u, p.wdt) : 0.f;
+  }
+
+  int s = find_seq(p.qsl, p.B, t0);
+  int64_t seq_start = p.qsl[s];
+  int64_t seq_end = p.qsl[s + 1];
+  float win[W > 1 ? W - 1 : 1][VEC];
+  bool skip = false;
+
+  // Loads the state history of sequence s and, for a tile starting inside
+  // the sequence, the preceding inputs, into the window.
+  auto enter = [&](int64_t t) {
+    const int64_t in_slot = resolve_slot(p, s, p.init_idx);
+    skip = p.slots && in_slot == p.pad;
+    const int64_t off = p.accepted ? p.accepted[s] - 1 : 0;
+    // History entries must lie inside a real slot and its state_len.
+    const bool valid = in_slot >= 0 && in_slot < p.lines && off >= 0 &&
+                       off + (W - 1) <= p.S;
+    const T* st = reinterpret_cast<const T*>(p.state) + in_slot * p.ssl + c0 * p.ssd;
+#pragma unroll
+    for (int j = 0; j < W - 1; ++j) {
+      const int64_t pos = t - (W - 1) + j;  // token this window entry holds
+      const int64_t v = (W - 1) + (pos - seq_start);  // index in cat(hist, x)
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) {
+        float h = 0.f;
+        if (v >= W - 1)
+          h = to_f32(reinterpret_cast<const T*>(p.x)[pos * p.sx + c0 + u]);
+        else if (valid && !skip)
+          h = to_f32(st[u * p.ssd + (off + v) * p.sss]);
+        win[j][u] = h;
+      }
+    }
+  };
+  enter(t0);
+
+  const T* xp = reinterpret_cast<const T*>(p.x) + c0;
+  T* op = reinterpret_cast<T*>(p.out) + c0;
+  for (int64_t t = t0; t < t_end; ++t) {
+    while (t >= seq_end) {  // crossed into the next (possibly empty) sequence
+      ++s;
+      seq_start = p.qsl[s];
+      seq_end = p.qsl[s + 1];
+      if (t >= seq_start && t < seq_end) enter(t);
+    }
+    const VT xv = *reinterpret_cast<const VT*>(xp + t * p.sx);
+    VT ov;
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) {
+      const float xc = to_f32(xv.v[u]);
+      float acc = bs[u];
+#pragma unroll
+      for (int j = 0; j < W - 1; ++j) acc = fmaf(win[j][u], wt[j][u], acc);
+      acc = fmaf(xc, wt[W - 1][u], acc);
+      ov.v[u] = from_f32<T>(act(acc, p.silu_on));
+#pragma unroll
+      for (int j = 0; j + 1 < W - 1; ++j) win[j][u] = win[j + 1][u];
+      if constexpr (W > 1) win[W - 2][u] = xc;
+    }
+    if (!skip) *reinterpret_cast<VT*>(op + t * p.so) = ov;
+  }
+}
+
+// Final conv state of each sequence (after the conv kernel has read every
+// history).  One lane per (sequence, channel).
+template <typename T>
+__global__ void __launch_bounds__(256) conv1d_varlen_state_kernel(VarlenParams p) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (gid >= static_cast<int64_t>(p.B) * p.D) return;
+  const int s = static_cast<int>(gid / p.D);
+  const int64_t c = gid - static_cast<int64_t>(s) * p.D;
+  const int64_t start = p.qsl[s];
+  const int64_t len = p.qsl[s + 1] - start;
+  if (len <= 0 || start < 0 || start + len > p.num_tokens) return;
+  const int64_t in_slot = resolve_slot(p, s, p.init_idx);
+  if (p.slots && in_slot == p.pad) return;
+  const int64_t out_slot = resolve_slot(p, s, p.last_idx);
+  if (out_slot < 0 || out_slot >= p.lines) return;
+  const bool in_valid = in_slot >= 0 && in_slot < p.lines;
+  const int64_t run = p.state_rule == 0
+                          ? p.eff_state_len - (p.max_query_len - len)
+                          : p.eff_state_len;
+  if (run <= 0 || run > p.S) return;
+  const int64_t off = p.accepted ? p.accepted[s] - 1 : 0;
+  const int64_t shift = p.accepted ? 1 : len;
+  T* dst = reinterpret_cast<T*>(p.state) + out_slot * p.ssl + c * p.ssd;
+  const T* src = reinterpret_cast<const T*>(p.state) + in_slot * p.ssl + c * p.ssd;
+  const T* x = reinterpret_cast<const T*>(p.x) + start * p.sx + c;
+  if (len >= run) {
+    for (int64_t i = 0; i < run; ++i) dst[i * p.sss] = x[(len - run + i) * p.sx];
+  } else {
+    const int64_t keep = run - len;
+    if (in_valid && off >= 0)
+      for (int64_t i = 0; i < keep && off + shift + i < p.S; ++i)
+        dst[i * p.sss] = src[(off + shift + i) * p.sss];  // reads run ahead
+    for (int64_t i = 0; i < len; ++i) dst[(keep + i) * p.sss] = x[i * p.sx];
+  }
+}
+
+template <typename T, int VEC>
+int launch_varlen_w(const VarlenParams& p, hipStream_t s) {
+  const dim3 grid(cdiv(p.D, 256 * VEC), cdiv(p.num_tokens, kTileT));
+  switch (p.W) {
+#define XK_W(n) \
+  case n: hipLaunchKernelGGL((conv1d_varlen_kernel<T, n, VEC>), grid, dim3(256), 0, s, p); break;
+    XK_W(1) XK_W(2) XK_W(3) XK_W(4) XK_W(5) XK_W(6) XK_W(7) XK_W(8)
+#undef XK_W
+    default: return XK_ERR_UNSUPPORTED;
+  }
+  int st = launch_status();
+  if (st) return st;
+  hipLaunchKernelGGL((conv1d_varlen_state_kernel<T>),
+                     dim3(cdiv(static_cast<int64_t>(p.B) * p.D, 256)), dim3(256), 0, s, p);
+  return launch_status();
+}
+
+template <typename T>
+int launch_varlen(const VarlenParams& p, hipStream_t s) {
+  constexpr int kV = 16 / sizeof(T);
+  const bool vec = p.D % kV == 0 && p.sx % kV == 0 && p.so % kV == 0 &&
+                   aligned(p.x, 16) && aligned(p.out, 16);
+  return vec ? launch_varlen_w<T, kV>(p, s) : launch_varlen_w<T, 1>(p, s);
+}
+
+}  // namespace
+}  // namespace xk
+
+using namespace xk;
+
+extern "C" int xk_causal_conv1d_update(
+    const void* x, int64_t stride_x_batch, int64_t stride_x_dim,
+    int64_t stride_x_token, void* conv_state, int64_t stride_state_line,
+    int64_t stride_state_dim, int64_t stride_state_token,
+    const void* weight, int64_t stride_w_dim, int64_t stride_w_tap,
+    const void* bias, xk_dtype wdtype, const int32_t* conv_state_indices,
+    int32_t pad_slot_id, int64_t num_cache_lines, void* out,
+    int64_t stride_o_batch,
+    int64_t stride_o_dim, int64_t stride_o_token, int64_t batch, int64_t dim,
+    int64_t seqlen, int64_t width, int64_t state_len, int activation,
+    xk_dtype dtype, void* stream) {
+  if (batch < 0 || dim <= 0 || seqlen <= 0 || width <= 0 ||
+      state_len < width - 1)
+    return XK_ERR_INVALID;
+  if (!is_float_dtype(dtype) || !is_float_dtype(wdtype)) return XK_ERR_UNSUPPORTED;
+  if (batch == 0) return XK_OK;
+  if (!x || !conv_state || !weight || !out) return XK_ERR_INVALID;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int eb = elem_bytes(dtype);
+  const bool w_ok = (wdtype == dtype && aligned(weight, 64)) ||
+                    (wdtype == XK_F32 && aligned(weight, 128));
+  const bool fast = width == 4 && state_len == 3 && seqlen == 1 &&
+                    stride_x_dim == 1 && stride_o_dim == 1 &&
+                    stride_state_dim == 3 && stride_state_token == 1 &&
+                    stride_w_dim == 4 && stride_w_tap == 1 && eb == 2 && w_ok &&
+                    dim % 8 == 0 && stride_x_batch == dim &&
+                    stride_o_batch == dim && stride_state_line % 8 == 0 &&
+                    aligned(x, 16) && aligned(out, 16) && aligned(conv_state, 16);
+  if (fast) {
+    const dim3 grid(cdiv(dim, 256 * 8), batch);
+#define XK_W4(T, WT)                                                            \
+  hipLaunchKernelGGL((conv1d_update_w4_kernel<T, WT>), grid, dim3(256), 0, s,   \
+                     static_cast<const T*>(x), static_cast<T*>(out),            \
+                     static_cast<T*>(conv_state), stride_state_line,            \
+                     static_cast<const WT*>(weight), wdtype, bias,              \
+                     conv_state_indices, pad_slot_id, num_cache_lines, batch,   \
+                     dim, activation)
+    if (dtype == XK_BF16) {
+      if (wdtype == XK_F32) XK_W4(bf16, float); else XK_W4(bf16, bf16);
+    } else {
+      if (wdtype == XK_F32) XK_W4(f16, float); else XK_W4(f16, f16);
+    }
+#undef XK_W4
+    return launch_status();
+  }
+  UpdateParams p{};
+  p.x = x;
+  p.sxb = stride_x_batch;
+  p.sxd = stride_x_dim;
+  p.sxt = stride_x_token;
+  p.out = out;
+  p.sob = stride_o_batch;
+  p.sod = stride_o_dim;
+  p.sot = stride_o_token;
+  p.state = conv_state;
+  p.ssl = stride_state_line;
+  p.ssd = stride_state_dim;
+  p.sss = stride_state_token;
+  p.w = weight;
+  p.swd = stride_w_dim;
+  p.sww = stride_w_tap;
+  p.wdt = wdtype;
+  p.bias = bias;
+  p.idx = conv_state_indices;
+  p.pad = pad_slot_id;
+  p.lines = num_cache_lines;
+  p.B = batch;
+  p.D = dim;
+  p.T = seqlen;
+  p.W = width;
+  p.S = state_len;
+  p.silu_on = activation;
+  const dim3 grid(cdiv(batch * dim, 256));
+  switch (dtype) {
+    case XK_F32: hipLaunchKernelGGL(conv1d_update_generic_kernel<float>, grid, dim3(256), 0, s, p); break;
+    case XK_BF16: hipLaunchKernelGGL(conv1d_update_generic_kernel<bf16>, grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL(conv1d_update_generic_kernel<f16>, grid, dim3(256), 0, s, p); break;
+  }
+  return launch_status();
+}
+
+extern "C" int xk_causal_conv1d_varlen(
+    const void* x, int64_t stride_x_token, int64_t num_tokens, void* out,
+    int64_t stride_o_token, void* conv_state, int64_t stride_state_line,
+    int64_t stride_state_dim, int64_t stride_state_token,
+    int64_t num_cache_lines, int64_t state_len, const void* weight,
+    int64_t stride_w_dim, int64_t stride_w_tap, const void* bias,
+    xk_dtype wdtype, const int32_t* query_start_loc, int64_t batch,
+    const int32_t* slot_table, int64_t slot_table_stride, int slot_table_2d,
+    const int32_t* initial_state_idx, const int32_t* last_state_idx,
+    const int32_t* num_accepted_tokens, int64_t dim, int64_t width,
+    int64_t max_query_len, int state_rule, int activation,
+    int32_t pad_slot_id, xk_dtype dtype, void* stream) {
+  if (batch < 0 || dim <= 0 || width < 1 || width > 8 || num_tokens < 0 ||
+      (state_rule != 0 && state_rule != 1) || max_query_len < 0)
+    return XK_ERR_INVALID;
+  if (!is_float_dtype(dtype) || !is_float_dtype(wdtype)) return XK_ERR_UNSUPPORTED;
+  const int64_t eff = width - 1 + (num_accepted_tokens ? max_query_len - 1 : 0);
+  if (eff > state_len) return XK_ERR_INVALID;  // state cannot hold the history
+  if (batch == 0 || num_tokens == 0) return XK_OK;
+  if (!x || !out || !conv_state || !weight || !query_start_loc)
+    return XK_ERR_INVALID;
+  VarlenParams p{};
+  p.x = x;
+  p.sx = stride_x_token;
+  p.out = out;
+  p.so = stride_o_token;
+  p.state = conv_state;
+  p.ssl = stride_state_line;
+  p.ssd = stride_state_dim;
+  p.sss = stride_state_token;
+  p.lines = num_cache_lines;
+  p.S = state_len;
+  p.w = weight;
+  p.swd = stride_w_dim;
+  p.sww = stride_w_tap;
+  p.wdt = wdtype;
+  p.bias = bias;
+  p.qsl = query_start_loc;
+  p.B = static_cast<int>(batch);
+  p.slots = slot_table;
+  p.slot_stride = slot_table_stride;
+  p.slot_2d = slot_table_2d;
+  p.init_idx = initial_state_idx;
+  p.last_idx = last_state_idx;
+  p.accepted = num_accepted_tokens;
+  p.D = dim;
+  p.W = static_cast<int>(width);
+  p.num_tokens = num_tokens;
+  p.max_query_len = static_cast<int>(max_query_len);
+  p.eff_state_len = static_cast<int>(eff);
+  p.state_rule = state_rule;
+  p.silu_on = activation;
+  p.pad = pad_slot_id;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case XK_F32: return launch_varlen<float>(p, s);
+    case XK_BF16: return launch_varlen<bf16>(p, s);
+    default: return launch_varlen<f16>(p, s);
+  }
+}

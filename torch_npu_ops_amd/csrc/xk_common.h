@@ -49,6 +49,12 @@ struct alignas(sizeof(T) * N) Vec {
   T v[N];
 };
 
+// Register array with no alignment requirement (any N).
+template <typename T, int N>
+struct Arr {
+  T v[N];
+};
+
 template <typename T, int N>
 __device__ __forceinline__ void load_vec_f32(const T* p, float (&out)[N]) {
   Vec<T, N> t = *reinterpret_cast<const Vec<T, N>*>(p);

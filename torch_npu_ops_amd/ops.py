@@ -195,6 +195,146 @@ def npu_split_rmsnorm_rope(input: torch.Tensor, sin: Optional[torch.Tensor],
     return q, k, v
 
 
+def npu_causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor,
+                             weight: torch.Tensor, activation: bool = True,
+                             bias: Optional[torch.Tensor] = None,
+                             cache_seqlens: Optional[torch.Tensor] = None,
+                             conv_state_indices: Optional[torch.Tensor] = None,
+                             num_accepted_tokens: Optional[torch.Tensor] = None,
+                             query_start_loc: Optional[torch.Tensor] = None,
+                             max_query_len: int = -1,
+                             intermediate_conv_window: Optional[torch.Tensor] = None,
+                             pad_slot_id: int = -1, validate_data: bool = False):
+    """Causal conv1d state update; conv_state is updated in place.
+
+    Mirrors npu_causal_conv1d_update
+    (triton_npu/torch_api/npu_triton_causal_conv1d_update.cpp:22-138): x is
+    [B, D] or [B, D, T]; query_start_loc is refused with zeros(1) (:41-45);
+    cache_seqlens / num_accepted_tokens are refused (:133-136).  Unlike the
+    reference, ``activation`` is honoured (its binaries ignore it, :38).
+    """
+    import warnings
+    if query_start_loc is not None:
+        warnings.warn("npu_causal_conv1d_update does not support query_start_loc")
+        return torch.zeros(1)
+    if cache_seqlens is not None or num_accepted_tokens is not None:
+        raise NotImplementedError("causal_conv1d_update does not support "
+                                  "cache_seqlens or num_accepted_tokens")
+    unsq = x.dim() == 2
+    xs = x.unsqueeze(-1) if unsq else x
+    B, D, T = xs.shape
+    W = weight.size(1)
+    S = conv_state.size(2)
+    if weight.size(0) != D or conv_state.size(1) != D:
+        raise ValueError("weight / conv_state dim mismatch")
+    out = torch.empty_like(xs)
+    idx = None
+    if conv_state_indices is not None:
+        idx = conv_state_indices.to(torch.int32).contiguous()
+    w = weight if weight.dtype in (x.dtype, torch.float32) else weight.to(x.dtype)
+    bvec = None
+    if bias is not None:
+        bvec = bias.to(w.dtype).contiguous()
+    st = lib().xk_causal_conv1d_update(
+        xs.data_ptr(), xs.stride(0), xs.stride(1), xs.stride(2),
+        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
+        conv_state.stride(2), w.data_ptr(), w.stride(0), w.stride(1), _ptr(bvec),
+        xk_dtype(w), _ptr(idx), int(pad_slot_id), conv_state.size(0),
+        out.data_ptr(), out.stride(0), out.stride(1), out.stride(2), B, D, T, W, S,
+        int(activation), xk_dtype(xs), _stream(x))
+    check(st, "xk_causal_conv1d_update")
+    return out.squeeze(-1) if unsq else out
+
+
+def npu_causal_conv1d_update_v2(x: torch.Tensor, conv_state: torch.Tensor,
+                                weight: torch.Tensor, activation: bool = True,
+                                bias: Optional[torch.Tensor] = None,
+                                conv_state_indices: Optional[torch.Tensor] = None,
+                                query_start_loc: Optional[torch.Tensor] = None,
+                                max_query_len: int = -1, pad_slot_id: int = -1,
+                                block_idx_last_scheduled_token: Optional[torch.Tensor] = None,
+                                initial_state_idx: Optional[torch.Tensor] = None,
+                                validate_data: bool = False,
+                                num_accepted_tokens: Optional[torch.Tensor] = None,
+                                state_rule: int = 0):
+    """Varlen causal conv1d with state slots (APC, spec decoding).
+
+    Mirrors npu_causal_conv1d_update_v2
+    (triton_npu/torch_api/npu_triton_causal_conv1d_update_v2.cpp:99-239) and
+    its input preparation (:31-90): with query_start_loc x is [tokens, D];
+    otherwise x is [B, D] or [B, D, T] and each batch row is one sequence.
+    conv_state [lines, D, state_len] is read and written in place (no
+    transposed copy).  ``state_rule`` 0 is the reference's final-state rule,
+    1 keeps the last width-1 inputs of every sequence (full prefill).
+    """
+    if weight.dim() != 2:
+        raise ValueError("causal_conv1d_update_v2 expects weight shape [dim, width].")
+    if (block_idx_last_scheduled_token is None) != (initial_state_idx is None):
+        raise ValueError("causal_conv1d_update_v2 expects both APC tensors or neither.")
+    if conv_state.dim() != 3:
+        raise ValueError("causal_conv1d_update_v2 expects conv_state shape "
+                         "[num_cache_lines, dim, state_len].")
+    dense = query_start_loc is None
+    if dense:
+        unsq = x.dim() == 2
+        xw = x.unsqueeze(-1) if unsq else x
+        B, D, T = xw.shape
+        xt = xw.transpose(1, 2).contiguous().view(B * T, D)
+        qsl = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=x.device)
+        mql = T
+    else:
+        if x.dim() != 2:
+            raise ValueError("causal_conv1d_update_v2 expects x to be 2D "
+                             "[num_tokens, dim] when query_start_loc is provided.")
+        qsl = query_start_loc.to(torch.int32).contiguous()
+        B = qsl.numel() - 1
+        D = x.size(1)
+        xt = x if x.stride(1) == 1 else x.contiguous()
+        mql = max_query_len
+        if mql < 0:
+            mql = int((qsl[1:] - qsl[:-1]).max().item()) if B > 0 else 0
+    W = weight.size(1)
+    if not 1 <= W <= 6:
+        raise ValueError(f"causal_conv1d_update_v2 expects width in [1, 6], got {W}")
+    if weight.size(0) != D or conv_state.size(1) != D:
+        raise ValueError("weight / conv_state dim mismatch")
+    slots, s2d, sstride = None, 0, 0
+    if conv_state_indices is not None:
+        slots = conv_state_indices.to(torch.int32).contiguous()
+        s2d = int(slots.dim() == 2)
+        sstride = slots.stride(0) if s2d else 1
+        if slots.size(0) != B:
+            raise ValueError("conv_state_indices batch mismatch")
+    last = init = acc = None
+    if block_idx_last_scheduled_token is not None:
+        last = block_idx_last_scheduled_token.to(torch.int32).contiguous()
+        init = initial_state_idx.to(torch.int32).contiguous()
+    if num_accepted_tokens is not None:
+        acc = num_accepted_tokens.to(torch.int32).contiguous()
+    # The kernel reads x in the state's dtype (reference :172) and the result
+    # is returned in x's original dtype (:238).
+    x_dtype = x.dtype
+    if xt.dtype != conv_state.dtype:
+        xt = xt.to(conv_state.dtype)
+    w = weight if weight.dtype in (xt.dtype, torch.float32) else weight.to(xt.dtype)
+    bvec = bias.to(w.dtype).contiguous() if bias is not None else None
+    out = torch.empty_like(xt)
+    st = lib().xk_causal_conv1d_varlen(
+        xt.data_ptr(), xt.stride(0), xt.size(0), out.data_ptr(), out.stride(0),
+        conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
+        conv_state.stride(2), conv_state.size(0), conv_state.size(2),
+        w.data_ptr(), w.stride(0), w.stride(1), _ptr(bvec), xk_dtype(w),
+        qsl.data_ptr(), B, _ptr(slots), sstride, s2d, _ptr(init), _ptr(last),
+        _ptr(acc), D, W, mql, int(state_rule), int(activation), int(pad_slot_id),
+        xk_dtype(xt), _stream(x))
+    check(st, "xk_causal_conv1d_varlen")
+    out = out.to(x_dtype)
+    if dense:
+        o = out.view(B, T, D).transpose(1, 2)
+        return o.squeeze(-1) if unsq else o.contiguous()
+    return out
+
+
 def npu_l2norm_last_dim(x: torch.Tensor, eps: float = 1e-6,
                         output_dtype: Optional[torch.dtype] = None):
     """x * rsqrt(sum(x^2) + eps) over the last dim.
