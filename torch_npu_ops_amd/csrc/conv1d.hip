@@ -182,6 +182,7 @@ struct VarlenParams {
   int state_rule;  // 0: reference rule, 1: prefill rule
   int silu_on;
   int32_t pad;
+  int w_vec;  // weights are [D, W] contiguous, x's dtype, 16-byte aligned
 };
 
 __device__ __forceinline__ int64_t resolve_slot(const VarlenParams& p, int s,
@@ -202,9 +203,31 @@ __device__ __forceinline__ int find_seq(const int32_t* qsl, int B, int64_t t) {
   return lo;
 }
 
-constexpr int kTileT = 32;  // tokens per lane per tile
+// Tokens per lane per tile (16 measured best on MI355X for 8192 channels:
+// longer tiles leave too few blocks, shorter ones repeat the prologue).
+#ifndef XK_CONV_TILE_T
+#define XK_CONV_TILE_T 16
+#endif
+constexpr int kTileT = XK_CONV_TILE_T;
+#ifndef XK_CONV_GROUP
+#define XK_CONV_GROUP 8
+#endif
+constexpr int kGroup = XK_CONV_GROUP;  // tokens loaded / computed together
+// Prefetch the next group of tokens while computing the current one (no
+// measurable gain at 32-token tiles; costs registers).
+#ifndef XK_CONV_DBUF
+#define XK_CONV_DBUF 0
+#endif
+constexpr bool kDoubleBuffer = XK_CONV_DBUF != 0;
+// Non-temporal hints for the streamed x loads / output stores (bit 0:
+// stores, bit 1: loads).
+#ifndef XK_CONV_NT
+#define XK_CONV_NT 3
+#endif
+constexpr bool kNtStore = (XK_CONV_NT & 1) != 0;
+constexpr bool kNtLoad = (XK_CONV_NT & 2) != 0;
 
-template <typename T, int W, int VEC>
+template <typename T, int W, int VEC, bool SILU>
 __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
   using VT = Vec<T, VEC>;
   const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC;
@@ -218,13 +241,33 @@ __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
   if (t0 >= t_end) return;
 
   float wt[W][VEC], bs[VEC];
+  constexpr int kWVec = 16 / sizeof(T);
+  if constexpr ((VEC * W) % kWVec == 0) {
+    if (p.w_vec) {
+      // Weights [D, W] in x's dtype: the lane's VEC*W taps are contiguous
+      // and 16-byte aligned, fetched as whole vectors.
+      const T* wp = reinterpret_cast<const T*>(p.w) + c0 * W;
 #pragma unroll
-  for (int u = 0; u < VEC; ++u) {
+      for (int q = 0; q < VEC * W / kWVec; ++q) {
+        const Vec<T, kWVec> wv = reinterpret_cast<const Vec<T, kWVec>*>(wp)[q];
 #pragma unroll
-    for (int j = 0; j < W; ++j)
-      wt[j][u] = load_as_f32(p.w, (c0 + u) * p.swd + j * p.sww, p.wdt);
-    bs[u] = p.bias ? load_as_f32(p.bias, c0 + u, p.wdt) : 0.f;
+        for (int e = 0; e < kWVec; ++e) {
+          const int i = q * kWVec + e;
+          wt[i % W][i / W] = to_f32(wv.v[e]);
+        }
+      }
+    }
   }
+  if (!p.w_vec || (VEC * W) % kWVec != 0) {
+#pragma unroll
+    for (int u = 0; u < VEC; ++u)
+#pragma unroll
+      for (int j = 0; j < W; ++j)
+        wt[j][u] = load_as_f32(p.w, (c0 + u) * p.swd + j * p.sww, p.wdt);
+  }
+#pragma unroll
+  for (int u = 0; u < VEC; ++u)
+    bs[u] = p.bias ? load_as_f32(p.bias, c0 + u, p.wdt) : 0.f;
 
   int s = find_seq(p.qsl, p.B, t0);
   int64_t seq_start = p.qsl[s];
@@ -246,29 +289,22 @@ __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
     for (int j = 0; j < W - 1; ++j) {
       const int64_t pos = t - (W - 1) + j;  // token this window entry holds
       const int64_t v = (W - 1) + (pos - seq_start);  // index in cat(hist, x)
+      if (v >= W - 1) {  // an earlier input of this sequence: one vector load
+        const VT hv = *reinterpret_cast<const VT*>(
+            reinterpret_cast<const T*>(p.x) + pos * p.sx + c0);
 #pragma unroll
-      for (int u = 0; u < VEC; ++u) {
-        float h = 0.f;
-        if (v >= W - 1)
-          h = to_f32(reinterpret_cast<const T*>(p.x)[pos * p.sx + c0 + u]);
-        else if (valid && !skip)
-          h = to_f32(st[u * p.ssd + (off + v) * p.sss]);
-        win[j][u] = h;
+        for (int u = 0; u < VEC; ++u) win[j][u] = to_f32(hv.v[u]);
+      } else {
+#pragma unroll
+        for (int u = 0; u < VEC; ++u)
+          win[j][u] = (valid && !skip) ? to_f32(st[u * p.ssd + (off + v) * p.sss]) : 0.f;
       }
     }
   };
   enter(t0);
 
-  const T* xp = reinterpret_cast<const T*>(p.x) + c0;
-  T* op = reinterpret_cast<T*>(p.out) + c0;
-  for (int64_t t = t0; t < t_end; ++t) {
-    while (t >= seq_end) {  // crossed into the next (possibly empty) sequence
-      ++s;
-      seq_start = p.qsl[s];
-      seq_end = p.qsl[s + 1];
-      if (t >= seq_start && t < seq_end) enter(t);
-    }
-    const VT xv = *reinterpret_cast<const VT*>(xp + t * p.sx);
+  // One token through the window: returns the output vector.
+  auto step = [&](const VT& xv) {
     VT ov;
 #pragma unroll
     for (int u = 0; u < VEC; ++u) {
@@ -277,12 +313,70 @@ __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
 #pragma unroll
       for (int j = 0; j < W - 1; ++j) acc = fmaf(win[j][u], wt[j][u], acc);
       acc = fmaf(xc, wt[W - 1][u], acc);
-      ov.v[u] = from_f32<T>(act(acc, p.silu_on));
+      if constexpr (SILU) acc = silu(acc);
+      ov.v[u] = from_f32<T>(acc);
 #pragma unroll
       for (int j = 0; j + 1 < W - 1; ++j) win[j][u] = win[j + 1][u];
       if constexpr (W > 1) win[W - 2][u] = xc;
     }
-    if (!skip) *reinterpret_cast<VT*>(op + t * p.so) = ov;
+    return ov;
+  };
+
+  const T* xp = reinterpret_cast<const T*>(p.x) + t0 * p.sx + c0;
+  T* op = reinterpret_cast<T*>(p.out) + t0 * p.so + c0;
+  int64_t t = t0;
+  while (t < t_end) {
+    if (t + kGroup <= seq_end && t + kGroup <= t_end) {
+      // Fast path: runs of kGroup tokens inside one sequence, straight-line
+      // code.  The next group's loads are issued before the current group
+      // is computed (two register sets), so a lane overlaps its own loads
+      // with its arithmetic.
+      VT xs[kGroup];
+#pragma unroll
+      for (int k = 0; k < kGroup; ++k)
+        xs[k] = kNtLoad ? ld_stream(reinterpret_cast<const VT*>(xp + k * p.sx))
+                        : *reinterpret_cast<const VT*>(xp + k * p.sx);
+      while (true) {
+        const bool more = kDoubleBuffer && t + 2 * kGroup <= seq_end &&
+                          t + 2 * kGroup <= t_end;
+        VT nx[kGroup];
+        if (more) {
+#pragma unroll
+          for (int k = 0; k < kGroup; ++k)
+            nx[k] = *reinterpret_cast<const VT*>(xp + (kGroup + k) * p.sx);
+        }
+#pragma unroll
+        for (int k = 0; k < kGroup; ++k) {
+          const VT ov = step(xs[k]);
+          if (!skip) {
+            if (kNtStore) st_stream(reinterpret_cast<VT*>(op + k * p.so), ov);
+            else *reinterpret_cast<VT*>(op + k * p.so) = ov;
+          }
+        }
+        t += kGroup;
+        xp += kGroup * p.sx;
+        op += kGroup * p.so;
+        if (!more) break;
+#pragma unroll
+        for (int k = 0; k < kGroup; ++k) xs[k] = nx[k];
+      }
+      continue;
+    }
+    // Slow path: one token, crossing into the next non-empty sequence when
+    // needed (its window is then pure history).
+    if (t >= seq_end) {
+      do {
+        ++s;
+        seq_start = p.qsl[s];
+        seq_end = p.qsl[s + 1];
+      } while (t >= seq_end);
+      enter(t);
+    }
+    const VT ov = step(*reinterpret_cast<const VT*>(xp));
+    if (!skip) *reinterpret_cast<VT*>(op) = ov;
+    ++t;
+    xp += p.sx;
+    op += p.so;
   }
 }
 
@@ -327,7 +421,12 @@ int launch_varlen_w(const VarlenParams& p, hipStream_t s) {
   const dim3 grid(cdiv(p.D, 256 * VEC), cdiv(p.num_tokens, kTileT));
   switch (p.W) {
 #define XK_W(n) \
-  case n: hipLaunchKernelGGL((conv1d_varlen_kernel<T, n, VEC>), grid, dim3(256), 0, s, p); break;
+  case n:                                                                       \
+    if (p.silu_on)                                                              \
+      hipLaunchKernelGGL((conv1d_varlen_kernel<T, n, VEC, true>), grid, dim3(256), 0, s, p); \
+    else                                                                        \
+      hipLaunchKernelGGL((conv1d_varlen_kernel<T, n, VEC, false>), grid, dim3(256), 0, s, p); \
+    break;
     XK_W(1) XK_W(2) XK_W(3) XK_W(4) XK_W(5) XK_W(6) XK_W(7) XK_W(8)
 #undef XK_W
     default: return XK_ERR_UNSUPPORTED;
@@ -340,10 +439,11 @@ int launch_varlen_w(const VarlenParams& p, hipStream_t s) {
 }
 
 template <typename T>
-int launch_varlen(const VarlenParams& p, hipStream_t s) {
+int launch_varlen(VarlenParams p, xk_dtype dt, hipStream_t s) {
   constexpr int kV = 16 / sizeof(T);
   const bool vec = p.D % kV == 0 && p.sx % kV == 0 && p.so % kV == 0 &&
                    aligned(p.x, 16) && aligned(p.out, 16);
+  p.w_vec = p.wdt == dt && p.swd == p.W && p.sww == 1 && aligned(p.w, 16);
   return vec ? launch_varlen_w<T, kV>(p, s) : launch_varlen_w<T, 1>(p, s);
 }
 
@@ -488,8 +588,8 @@ extern "C" int xk_causal_conv1d_varlen(
   p.pad = pad_slot_id;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case XK_F32: return launch_varlen<float>(p, s);
-    case XK_BF16: return launch_varlen<bf16>(p, s);
-    default: return launch_varlen<f16>(p, s);
+    case XK_F32: return launch_varlen<float>(p, dtype, s);
+    case XK_BF16: return launch_varlen<bf16>(p, dtype, s);
+    default: return launch_varlen<f16>(p, dtype, s);
   }
 }

@@ -107,34 +107,6 @@ __device__ __forceinline__ void vec_sums(const Vec<T, VEC>& v, float& s1,
   }
 }
 
-// Streaming (read-once / write-once) vector access: non-temporal hints keep
-// x, z and y from displacing reusable lines in L2 and the Infinity Cache.
-typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-template <int BYTES> struct RawOf { using type = void; };
-template <> struct RawOf<4> { using type = unsigned int; };
-template <> struct RawOf<8> { using type = u32x2; };
-template <> struct RawOf<16> { using type = u32x4; };
-
-template <typename V>
-__device__ __forceinline__ V ld_stream(const V* p) {
-  using U = typename RawOf<sizeof(V)>::type;
-  if constexpr (std::is_void<U>::value) {
-    return *p;
-  } else {
-    return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const U*>(p)));
-  }
-}
-template <typename V>
-__device__ __forceinline__ void st_stream(V* p, const V& v) {
-  using U = typename RawOf<sizeof(V)>::type;
-  if constexpr (std::is_void<U>::value) {
-    *p = v;
-  } else {
-    __builtin_nontemporal_store(__builtin_bit_cast(U, v), reinterpret_cast<U*>(p));
-  }
-}
-
 // One (row, group) item per team.  FULL: the group is exactly
 // NV * TPG * VEC elements, so no lane ever needs a bounds mask and all
 // loads of an item issue back to back with no branch between them.

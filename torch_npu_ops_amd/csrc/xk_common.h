@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "xk_ops.h"
 
 namespace xk {
@@ -49,6 +51,36 @@ struct alignas(sizeof(T) * N) Vec {
   T v[N];
 };
 
+// Streaming (read-once / write-once) vector access: non-temporal hints keep
+// streamed tensors from displacing reusable lines in L2 and the Infinity
+// Cache.  Vectors of 4, 8 or 16 bytes; other sizes fall back to plain
+// accesses.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <int BYTES> struct RawOf { using type = void; };
+template <> struct RawOf<4> { using type = unsigned int; };
+template <> struct RawOf<8> { using type = u32x2; };
+template <> struct RawOf<16> { using type = u32x4; };
+
+template <typename V>
+__device__ __forceinline__ V ld_stream(const V* p) {
+  using U = typename RawOf<sizeof(V)>::type;
+  if constexpr (std::is_void<U>::value) {
+    return *p;
+  } else {
+    return __builtin_bit_cast(V, __builtin_nontemporal_load(reinterpret_cast<const U*>(p)));
+  }
+}
+template <typename V>
+__device__ __forceinline__ void st_stream(V* p, const V& v) {
+  using U = typename RawOf<sizeof(V)>::type;
+  if constexpr (std::is_void<U>::value) {
+    *p = v;
+  } else {
+    __builtin_nontemporal_store(__builtin_bit_cast(U, v), reinterpret_cast<U*>(p));
+  }
+}
+
 // Register array with no alignment requirement (any N).
 template <typename T, int N>
 struct Arr {
@@ -81,13 +113,19 @@ __device__ __forceinline__ float group_sum(float v) {
   return v;
 }
 
-__device__ __forceinline__ float silu(float x) {
-  return x / (1.0f + __expf(-x));
+// Hardware reciprocal (v_rcp_f32, ~1 ulp): sigmoid/SiLU feed bf16/fp16 or
+// tolerance-checked fp32 outputs, so the IEEE division sequence (about ten
+// instructions) is not needed.  exp(-x) overflowing to +inf gives rcp = 0,
+// the correct limit.
+__device__ __forceinline__ float fast_rcp(float x) {
+  return __builtin_amdgcn_rcpf(x);
 }
 
 __device__ __forceinline__ float sigmoid(float x) {
-  return 1.0f / (1.0f + __expf(-x));
+  return fast_rcp(1.0f + __expf(-x));
 }
+
+__device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
 
 inline int launch_status() {
   hipError_t e = hipGetLastError();
