@@ -303,8 +303,132 @@ class ConvDecodeCase(Case):
                 "full config 3b (256 x 8192), fp32", 1.0)
 
 
+class GdnDecodeInputs:
+    """BASELINE config 5 inputs (shared by the fused and unfused cases)."""
+    B, H, HV, K, V, W = 256, 16, 32, 128, 128, 4
+
+    def __init__(self):
+        import torch.nn.functional as F
+        g = torch.Generator().manual_seed(0)
+        D = 2 * self.H * self.K + self.HV * self.V
+        self.D = D
+        self.x = _randn((self.B, D), g, torch.bfloat16)
+        self.cs = _randn((self.B, D, self.W - 1), g, torch.bfloat16)
+        self.cw = _randn((D, self.W), g, torch.bfloat16, 0.5)
+        self.gate = (-F.softplus(torch.randn(self.B, self.HV, generator=g))).to(torch.bfloat16)
+        self.beta = torch.sigmoid(torch.randn(self.B, self.HV, generator=g)).to(torch.bfloat16)
+        self.state = torch.randn(self.B, self.HV, self.K, self.V, generator=g) * 0.02
+        self.idx = torch.arange(self.B, dtype=torch.int32)
+
+
+class GdnDecodeFusedCase(Case):
+    name = "gdn_decode_fused"
+    config = ("config 5: recurrent GDN decode fused with causal_conv1d update, "
+              "batch 256, 16 qk / 32 v heads, head_dim 128, fp32 state "
+              "[256,32,128,128] in place, bf16 mixed_qkv/g/beta")
+    kernel = "gdn_conv_decode_kernel"
+    I = GdnDecodeInputs
+    # state r/w + mixed_qkv + conv_state r/w + conv_w + g/beta + o
+    algo_bytes = (I.B * I.HV * I.K * I.V * 4 * 2 + I.B * 8192 * 2
+                  + I.B * 8192 * 3 * 2 * 2 + 8192 * 4 * 2 + I.B * I.HV * 2 * 2
+                  + I.B * I.HV * I.V * 2)
+
+    def __init__(self):
+        self.inp = GdnDecodeInputs()
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        a = self.inp
+        cw, g, beta, idx = a.cw.to(dev), a.gate.to(dev), a.beta.to(dev), a.idx.to(dev)
+        out = []
+        for _ in range(n):
+            x, cs, st = a.x.to(dev), a.cs.to(dev), a.state.to(dev)
+            o = torch.empty(a.B, a.HV, a.V, dtype=torch.bfloat16, device=dev)
+
+            def run(x=x, cs=cs, st=st, o=o):
+                _ok(lib.xk_gdn_conv_decode(
+                    x.data_ptr(), a.D, cs.data_ptr(), cs.stride(0), cs.stride(1),
+                    cs.stride(2), a.B, a.W - 1, cw.data_ptr(), a.W, 1, None,
+                    _lib.XK_BF16, a.W, idx.data_ptr(), -1, g.data_ptr(),
+                    _lib.XK_BF16, beta.data_ptr(), _lib.XK_BF16, st.data_ptr(),
+                    st.stride(0), a.B, idx.data_ptr(), o.data_ptr(), a.B, a.H,
+                    a.HV, a.K, a.V, a.K ** -0.5, 1, _lib.XK_BF16, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import conv1d as oc
+        from oracle import gdn as og
+        a = self.inp
+        n = 16  # bounded sample: 16 of the 256 batch rows
+
+        def run():
+            y, _ = oc.causal_conv1d_update(a.x[:n], a.cs[:n], a.cw, None, True,
+                                           a.idx[:n])
+            q = y[:, :a.H * a.K].reshape(n, a.H, a.K)
+            k = y[:, a.H * a.K:2 * a.H * a.K].reshape(n, a.H, a.K)
+            v = y[:, 2 * a.H * a.K:].reshape(n, a.HV, a.V)
+            og.recurrent_gdn(q, k, v, a.gate[:n], a.beta[:n], a.K ** -0.5,
+                             a.state[:n], T=1, ssm_state_indices=a.idx[:n],
+                             dtype=torch.float32)
+        return run, f"{n} of 256 batch rows (conv update + split + l2norm + GDN step, fp32)", a.B / n
+
+
+class GdnRecurrentCase(Case):
+    name = "gdn_recurrent"
+    config = ("config 5 (unfused a7 form): fused_recurrent_gated_delta_rule, "
+              "256 sequences x 1 token, 16 qk / 32 v heads, head_dim 128, "
+              "fp32 state in place, in-kernel l2norm")
+    kernel = "gdn_recurrent_kernel"
+    I = GdnDecodeInputs
+    # state r/w + q/k/v + g/beta + o
+    algo_bytes = (I.B * I.HV * I.K * I.V * 4 * 2 + I.B * (2 * I.H * I.K + I.HV * I.V) * 2
+                  + I.B * I.HV * 2 * 2 + I.B * I.HV * I.V * 2)
+
+    def __init__(self):
+        a = self.inp = GdnDecodeInputs()
+        self.q = a.x[:, :a.H * a.K].reshape(a.B, a.H, a.K).contiguous()
+        self.k = a.x[:, a.H * a.K:2 * a.H * a.K].reshape(a.B, a.H, a.K).contiguous()
+        self.v = a.x[:, 2 * a.H * a.K:].reshape(a.B, a.HV, a.V).contiguous()
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        a = self.inp
+        q, k, v = self.q.to(dev), self.k.to(dev), self.v.to(dev)
+        g, beta, idx = a.gate.to(dev), a.beta.to(dev), a.idx.to(dev)
+        cu = torch.arange(a.B + 1, dtype=torch.int32, device=dev)
+        out = []
+        for _ in range(n):
+            st = a.state.to(dev)
+            o = torch.empty(a.B, a.HV, a.V, dtype=torch.bfloat16, device=dev)
+
+            def run(st=st, o=o):
+                _ok(lib.xk_gdn_recurrent(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.XK_BF16,
+                    g.data_ptr(), _lib.XK_BF16, beta.data_ptr(), _lib.XK_BF16,
+                    o.data_ptr(), st.data_ptr(), st.stride(0), st.data_ptr(),
+                    st.stride(0), a.B, cu.data_ptr(), _lib.XK_I32, idx.data_ptr(),
+                    1, 0, None, a.B, 0, a.H, a.HV, a.K, a.V, a.K ** -0.5, 1, 1,
+                    _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import gdn as og
+        a = self.inp
+        n = 16
+
+        def run():
+            og.recurrent_gdn(self.q[:n], self.k[:n], self.v[:n], a.gate[:n],
+                             a.beta[:n], a.K ** -0.5, a.state[:n], T=1,
+                             ssm_state_indices=a.idx[:n], dtype=torch.float32)
+        return run, f"{n} of 256 sequences, fp32", a.B / n
+
+
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
-                             ConvDecodeCase)}
+                             ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase)}
 HEADLINE = "layer_norm_fwd"
 
 

@@ -170,6 +170,60 @@ int xk_causal_conv1d_varlen(
     int64_t max_query_len, int state_rule, int activation,
     int32_t pad_slot_id, xk_dtype dtype, void* stream);
 
+/* ------------------------------------------------------------------------
+ * a7. Gated delta rule, recurrent form (decode, speculative windows).
+ * Replaces xllm::kernel::npu::npu_fused_recurrent_gated_delta_rule
+ *   (triton_npu/torch_api/triton_ops_api.h:81-93,
+ *    npu_triton_recurrent_gated_delta_rule.cpp:54-247).
+ *   q, k : [tokens, H, K]; v, o : [tokens, HV, V] (dtype); g, beta :
+ *   [tokens, HV] (g_dtype / beta_dtype; beta NULL = 1).  Sequences are
+ *   cu_seqlens[n]..cu_seqlens[n+1] (int32/int64) or, when NULL, N runs of T
+ *   tokens.  States are fp32 [*, HV, K, V]: the initial state of sequence n
+ *   is initial_state[slot] with slot = ssm_state_indices[n*stride_idx_seq +
+ *   c*stride_idx_tok] (c = num_accepted_tokens[n]-1 with speculative
+ *   decoding, else 0; slot = n without indices); out-of-range slots start
+ *   from zero and are not written.  inplace_final_state != 0 writes the
+ *   state into final_state (normally == initial_state) at that slot, or
+ *   after every token t at column t when stride_idx_tok != 0; otherwise
+ *   final_state is a dense [N, HV, K, V].  use_qk_l2norm normalises q and k
+ *   by 1/sqrt(sum^2 + 1e-6) before `scale`.  (K, V) in {64, 128}^2.
+ */
+int xk_gdn_recurrent(
+    const void* q, const void* k, const void* v, xk_dtype dtype, const void* g,
+    xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype, void* o,
+    const float* initial_state, int64_t stride_h0_slot, float* final_state,
+    int64_t stride_ht_slot, int64_t num_slots, const void* cu_seqlens,
+    xk_dtype cu_dtype, const int32_t* ssm_state_indices, int64_t stride_idx_seq,
+    int64_t stride_idx_tok, const int32_t* num_accepted_tokens, int64_t N,
+    int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+    int use_qk_l2norm, int inplace_final_state, void* stream);
+
+/* ------------------------------------------------------------------------
+ * a8. One decode step of the gated delta rule fused with the causal conv1d
+ * update of its mixed q/k/v projection (no single reference function: the
+ * composition of npu_causal_conv1d_update, the [q | k | v] channel split of
+ * triton_npu/triton_src/test_fused_qkvzba_split_reshape.py:493-500 and
+ * npu_fused_recurrent_gated_delta_rule).
+ *   mixed_qkv : [B, 2*H*K + HV*V] (row stride), conv over the state
+ *   [lines, D, conv_state_len] with weight [D, width] (+ bias) and SiLU, the
+ *   state shifted in place; then q = ch[0:H*K], k = ch[H*K:2*H*K],
+ *   v = ch[2*H*K:], l2norm (optional) and one GDN step on
+ *   ssm_state[ssm_state_indices[b]] (fp32 [slots, HV, K, V], in place).
+ *   g, beta : [B, HV].  o : [B, HV, V].  Rows whose conv slot equals
+ *   pad_slot_id are skipped.  K = V = 128, HV/H <= 16.
+ */
+int xk_gdn_conv_decode(
+    const void* mixed_qkv, int64_t stride_x_row, void* conv_state,
+    int64_t stride_cs_line, int64_t stride_cs_dim, int64_t stride_cs_tok,
+    int64_t conv_lines, int64_t conv_state_len, const void* conv_weight,
+    int64_t stride_w_dim, int64_t stride_w_tap, const void* conv_bias,
+    xk_dtype w_dtype, int64_t width, const int32_t* conv_state_indices,
+    int32_t pad_slot_id, const void* g, xk_dtype g_dtype, const void* beta,
+    xk_dtype beta_dtype, float* ssm_state, int64_t stride_state_slot,
+    int64_t num_slots, const int32_t* ssm_state_indices, void* o, int64_t B,
+    int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+    int use_qk_l2norm, xk_dtype dtype, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

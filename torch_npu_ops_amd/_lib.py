@@ -50,6 +50,13 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         [P, I64, I64, P, I64, P, I64, I64, I64, I64, I64, P, I64, I64, P, INT,
          P, I64, P, I64, INT, P, P, P, I64, I64, I64, INT, INT, I32, INT, P],
         INT),
+    "xk_gdn_recurrent": (
+        [P, P, P, INT, P, INT, P, INT, P, P, I64, P, I64, I64, P, INT, P, I64,
+         I64, P, I64, I64, I64, I64, I64, I64, F32, INT, INT, P], INT),
+    "xk_gdn_conv_decode": (
+        [P, I64, P, I64, I64, I64, I64, I64, P, I64, I64, P, INT, I64, P, I32,
+         P, INT, P, INT, P, I64, I64, P, P, I64, I64, I64, I64, I64, F32, INT,
+         INT, P], INT),
 }
 
 _LIB = None

@@ -1,0 +1,560 @@
+// Gated delta rule, recurrent form (decode / short speculative windows),
+// and the decode step fused with the causal conv1d update, for gfx950.
+//
+// Per token (reference kernel triton_npu/triton_src/
+// test_fused_recurrent_gated_delta_rule.py:125-164, CPU golden
+// triton_npu/test/triton_recurrent_gated_delta_rule_test.cpp:47-115):
+//   q, k <- q/sqrt(sum q^2 + 1e-6), k/sqrt(sum k^2 + 1e-6)   (if l2norm)
+//   q    <- q * scale
+//   h    <- exp(g) * h                       h: [K, V] fp32 per (slot, head)
+//   v'   <- beta * (v - h^T k)
+//   h    <- h + k v'^T
+//   o    <- h^T q
+// GQA: v-head hv reads qk-head hv / (HV / H).  State slots come from
+// ssm_state_indices; with num_accepted_tokens (speculative decoding) the
+// initial state is column accepted-1 and the state after token t goes to
+// column t (..._spec_fwd_kernel, :257-307).
+//
+// Design (HBM-bound state streaming): one 256-lane block per (sequence,
+// v-head) keeps the whole K x V fp32 state in registers, K*V/256 values per
+// lane laid out so that each row of V values is contiguous across V/4
+// lanes (16-byte accesses, 1 KB per wave per instruction).  h^T k and h^T q
+// of the decayed state come out of one pass over the registers and one
+// cross-wave LDS reduction (o = (e^g h)^T q + (k.q) v', so the update and
+// the output need no second pass); the rank-1 update is applied in
+// registers and the state is written back once.  State traffic uses
+// non-temporal hints: it is read and written exactly once per call.
+#include "xk_common.h"
+
+namespace xk {
+namespace {
+
+constexpr int kThreads = 256;
+
+// Per-lane share of a K x V state tile.
+template <int K, int V>
+struct Tile {
+  static constexpr int kLanesPerRow = V / 4;               // float4 per lane
+  static constexpr int kRowsPerPass = kThreads / kLanesPerRow;
+  static constexpr int kPasses = K / kRowsPerPass;
+  static_assert(V % 4 == 0 && kLanesPerRow <= kWave && kWave % kLanesPerRow == 0,
+                "row of V must fit a wave");
+  static_assert(K % kRowsPerPass == 0, "K must be a multiple of rows per pass");
+  float h[kPasses][4];
+};
+
+// LDS shared by one block: normalised q/k (fp32), v, the reduction scratch
+// and the per-column results.
+template <int K, int V>
+struct Smem {
+  float q[K];
+  float k[K];
+  float v[V];
+  float red[2][kThreads / kWave][V];  // per-wave partials of h^T k, h^T q
+  float kh[V];
+  float qh[V];
+  float scal[4];  // k.q, ||q||^2, ||k||^2
+};
+
+template <typename T>
+__device__ __forceinline__ float ldf(const void* p, int64_t i) {
+  return to_f32(reinterpret_cast<const T*>(p)[i]);
+}
+
+// One token of the recurrence on the register tile.  Inputs (q, k already
+// normalised and q scaled) are in sm.q / sm.k / sm.v.  Writes o[V] through
+// `out` (fp32 values, converted by the caller's store functor).
+template <int K, int V, typename StoreO>
+__device__ __forceinline__ void gdn_token(Tile<K, V>& t, Smem<K, V>& sm,
+                                          float decay, float beta, StoreO store_o) {
+  using TL = Tile<K, V>;
+  const int tid = threadIdx.x;
+  const int c4 = tid % TL::kLanesPerRow;  // column group (4 columns)
+  const int r0 = tid / TL::kLanesPerRow;  // first row
+  const int wid = tid / kWave;
+  __syncthreads();  // sm.q / sm.k / sm.v of this token are complete
+
+  float pk[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < TL::kPasses; ++i) {
+    const int r = r0 + i * TL::kRowsPerPass;
+    const float kr = sm.k[r], qr = sm.q[r];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      t.h[i][c] *= decay;
+      pk[c] = fmaf(t.h[i][c], kr, pk[c]);
+      pq[c] = fmaf(t.h[i][c], qr, pq[c]);
+    }
+  }
+  // Reduce over the rows held by the other lanes of this wave (same c4).
+#pragma unroll
+  for (int o = TL::kLanesPerRow; o < kWave; o <<= 1)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      pk[c] += __shfl_xor(pk[c], o, kWave);
+      pq[c] += __shfl_xor(pq[c], o, kWave);
+    }
+  if ((tid % kWave) < TL::kLanesPerRow) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      sm.red[0][wid][c4 * 4 + c] = pk[c];
+      sm.red[1][wid][c4 * 4 + c] = pq[c];
+    }
+  }
+  __syncthreads();
+  if (tid < V) {
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) {
+      a += sm.red[0][w][tid];
+      b += sm.red[1][w][tid];
+    }
+    // v' = beta (v - h^T k);  o = h^T q + (k.q) v'
+    const float vn = beta * (sm.v[tid] - a);
+    sm.kh[tid] = vn;
+    store_o(tid, b + sm.scal[0] * vn);
+  }
+  __syncthreads();
+  float vn[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) vn[c] = sm.kh[c4 * 4 + c];
+#pragma unroll
+  for (int i = 0; i < TL::kPasses; ++i) {
+    const float kr = sm.k[r0 + i * TL::kRowsPerPass];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) t.h[i][c] = fmaf(kr, vn[c], t.h[i][c]);
+  }
+}
+
+template <int K, int V>
+__device__ __forceinline__ void load_tile(Tile<K, V>& t, const float* base) {
+  using TL = Tile<K, V>;
+  const int c4 = threadIdx.x % TL::kLanesPerRow;
+  const int r0 = threadIdx.x / TL::kLanesPerRow;
+#pragma unroll
+  for (int i = 0; i < TL::kPasses; ++i) {
+    const Vec<float, 4> v = ld_stream(reinterpret_cast<const Vec<float, 4>*>(
+        base + static_cast<int64_t>(r0 + i * TL::kRowsPerPass) * V + c4 * 4));
+#pragma unroll
+    for (int c = 0; c < 4; ++c) t.h[i][c] = v.v[c];
+  }
+}
+
+template <int K, int V>
+__device__ __forceinline__ void zero_tile(Tile<K, V>& t) {
+#pragma unroll
+  for (int i = 0; i < Tile<K, V>::kPasses; ++i)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) t.h[i][c] = 0.f;
+}
+
+template <int K, int V>
+__device__ __forceinline__ void store_tile(const Tile<K, V>& t, float* base) {
+  using TL = Tile<K, V>;
+  const int c4 = threadIdx.x % TL::kLanesPerRow;
+  const int r0 = threadIdx.x / TL::kLanesPerRow;
+#pragma unroll
+  for (int i = 0; i < TL::kPasses; ++i) {
+    Vec<float, 4> v;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v.v[c] = t.h[i][c];
+    st_stream(reinterpret_cast<Vec<float, 4>*>(
+                  base + static_cast<int64_t>(r0 + i * TL::kRowsPerPass) * V + c4 * 4),
+              v);
+  }
+}
+
+// Loads q and k of one token (raw), then l2-normalises (optional) and
+// scales q.  Block-wide; ends with a barrier.
+template <int K, int V, typename LoadQK>
+__device__ __forceinline__ void prep_qk(Smem<K, V>& sm, LoadQK load, bool l2norm,
+                                        float scale) {
+  const int tid = threadIdx.x;
+  // The previous token's readers of sm.q / sm.k / sm.scal are done.
+  __syncthreads();
+  if (tid < K) {
+    const float qv = load(0, tid), kv = load(1, tid);
+    sm.q[tid] = qv;
+    sm.k[tid] = kv;
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    float sq = 0.f, sk = 0.f, kq = 0.f;
+    for (int i = tid; i < K; i += kWave) {
+      sq = fmaf(sm.q[i], sm.q[i], sq);
+      sk = fmaf(sm.k[i], sm.k[i], sk);
+      kq = fmaf(sm.q[i], sm.k[i], kq);
+    }
+    sq = group_sum<kWave>(sq);
+    sk = group_sum<kWave>(sk);
+    kq = group_sum<kWave>(kq);
+    if (tid == 0) {
+      const float rq = l2norm ? 1.0f / sqrtf(sq + 1e-6f) : 1.0f;
+      const float rk = l2norm ? 1.0f / sqrtf(sk + 1e-6f) : 1.0f;
+      sm.scal[1] = rq * scale;
+      sm.scal[2] = rk;
+      sm.scal[0] = kq * rq * rk * scale;  // (k_hat . q_hat) * scale
+    }
+  }
+  __syncthreads();
+  if (tid < K) {
+    sm.q[tid] *= sm.scal[1];
+    sm.k[tid] *= sm.scal[2];
+  }
+  // sm.q / sm.k are read by other lanes in gdn_token after its first
+  // barrier; sm.v must be written by the caller before that barrier too.
+}
+
+// ---------------------------------------------------------------------------
+// a7: recurrent GDN over varlen sequences.
+// ---------------------------------------------------------------------------
+struct RecParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* g;
+  const void* beta;
+  void* o;
+  const float* h0;
+  float* ht;
+  int64_t h0_slot_stride, ht_slot_stride;
+  int64_t slots;  // rows of the state pool (valid slot range)
+  const void* cu;
+  int cu_i64;
+  const int32_t* idx;
+  int64_t idx_s0, idx_s1;
+  const int32_t* accepted;
+  int64_t N, T;  // sequences; tokens per sequence when cu == NULL
+  int H, HV;
+  float scale;
+  int l2norm;
+  int inplace;
+};
+
+template <int K, int V, typename T, typename GT, typename BT>
+__global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
+  __shared__ Smem<K, V> sm;
+  const int64_t n = blockIdx.x / p.HV;
+  const int hv = static_cast<int>(blockIdx.x % p.HV);
+  const int hq = hv / (p.HV / p.H);
+  int64_t bos, len;
+  if (p.cu) {
+    const int64_t a = p.cu_i64 ? reinterpret_cast<const int64_t*>(p.cu)[n]
+                               : reinterpret_cast<const int32_t*>(p.cu)[n];
+    const int64_t b = p.cu_i64 ? reinterpret_cast<const int64_t*>(p.cu)[n + 1]
+                               : reinterpret_cast<const int32_t*>(p.cu)[n + 1];
+    bos = a;
+    len = b - a;
+  } else {
+    bos = n * p.T;
+    len = p.T;
+  }
+  if (len <= 0) return;  // whole block exits together
+
+  const int64_t first_col = p.accepted ? p.accepted[n] - 1 : 0;
+  auto slot_of = [&](int64_t col) -> int64_t {
+    return p.idx ? p.idx[n * p.idx_s0 + col * p.idx_s1] : n;
+  };
+  Tile<K, V> t;
+  const int64_t s0 = slot_of(first_col);
+  const bool s0_ok = p.h0 && s0 >= 0 && s0 < p.slots && first_col >= 0;
+  if (s0_ok)
+    load_tile<K, V>(t, p.h0 + s0 * p.h0_slot_stride + static_cast<int64_t>(hv) * K * V);
+  else
+    zero_tile<K, V>(t);
+
+  // Per-token state writes: in place with a per-token slot column (2-D
+  // indices or speculative decoding); otherwise once at the end.
+  const bool per_token = p.inplace && p.idx && p.idx_s1 != 0;
+  for (int64_t i = 0; i < len; ++i) {
+    const int64_t tok = bos + i;
+    prep_qk<K, V>(sm, [&](int which, int e) {
+      const void* src = which == 0 ? p.q : p.k;
+      return ldf<T>(src, (tok * p.H + hq) * K + e);
+    }, p.l2norm, p.scale);
+    if (threadIdx.x < V) sm.v[threadIdx.x] = ldf<T>(p.v, (tok * p.HV + hv) * V + threadIdx.x);
+    const float decay = __expf(ldf<GT>(p.g, tok * p.HV + hv));
+    const float beta = p.beta ? ldf<BT>(p.beta, tok * p.HV + hv) : 1.0f;
+    T* o = reinterpret_cast<T*>(p.o) + (tok * p.HV + hv) * V;
+    gdn_token<K, V>(t, sm, decay, beta, [&](int c, float val) { o[c] = from_f32<T>(val); });
+    if (per_token) {
+      const int64_t sl = slot_of(i);
+      if (sl >= 0 && sl < p.slots)
+        store_tile<K, V>(t, p.ht + sl * p.ht_slot_stride + static_cast<int64_t>(hv) * K * V);
+    }
+  }
+  if (!per_token) {
+    if (p.inplace) {
+      if (s0 >= 0 && s0 < p.slots && first_col >= 0)
+        store_tile<K, V>(t, p.ht + s0 * p.ht_slot_stride + static_cast<int64_t>(hv) * K * V);
+    } else {
+      store_tile<K, V>(t, p.ht + n * p.ht_slot_stride + static_cast<int64_t>(hv) * K * V);
+    }
+  }
+}
+
+template <int K, int V, typename T, typename GT>
+int rec_beta(const RecParams& p, xk_dtype bdt, hipStream_t s) {
+  const dim3 grid(p.N * p.HV);
+  switch (bdt) {
+    case XK_F32: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, float>), grid, dim3(kThreads), 0, s, p); break;
+    case XK_BF16: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, bf16>), grid, dim3(kThreads), 0, s, p); break;
+    case XK_F16: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, f16>), grid, dim3(kThreads), 0, s, p); break;
+    default: return XK_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+template <int K, int V, typename T>
+int rec_g(const RecParams& p, xk_dtype gdt, xk_dtype bdt, hipStream_t s) {
+  switch (gdt) {
+    case XK_F32: return rec_beta<K, V, T, float>(p, bdt, s);
+    case XK_BF16: return rec_beta<K, V, T, bf16>(p, bdt, s);
+    case XK_F16: return rec_beta<K, V, T, f16>(p, bdt, s);
+    default: return XK_ERR_UNSUPPORTED;
+  }
+}
+
+template <int K, int V>
+int rec_t(const RecParams& p, xk_dtype dt, xk_dtype gdt, xk_dtype bdt, hipStream_t s) {
+  switch (dt) {
+    case XK_BF16: return rec_g<K, V, bf16>(p, gdt, bdt, s);
+    case XK_F16: return rec_g<K, V, f16>(p, gdt, bdt, s);
+    case XK_F32: return rec_g<K, V, float>(p, gdt, bdt, s);
+    default: return XK_ERR_UNSUPPORTED;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a8: decode step fused with the conv1d update.  One block per (batch row,
+// qk-head): it owns the conv channels of that q head, that k head and the
+// HV/H v heads of the group, so every conv channel and every state tile is
+// read and written by exactly one block.
+// ---------------------------------------------------------------------------
+struct FusedParams {
+  const void* x;  // mixed_qkv [B, D] (D = 2*H*K + HV*V)
+  int64_t sx;
+  void* conv_state;  // [lines, D, S]
+  int64_t cs_line, cs_dim, cs_tok;
+  int64_t conv_lines;
+  int S;  // conv state_len
+  const void* w;  // [D, W]
+  int64_t w_dim, w_tap;
+  const void* cbias;  // [D] or NULL
+  xk_dtype wdt;
+  const int32_t* conv_idx;
+  int W;
+  const void* g;  // [B, HV]
+  const void* beta;
+  float* state;  // [slots, HV, K, V]
+  int64_t st_slot_stride;
+  int64_t slots;
+  const int32_t* ssm_idx;
+  void* o;  // [B, HV, V]
+  int64_t B;
+  int H, HV;
+  float scale;
+  int l2norm;
+  int32_t pad;
+};
+
+template <int K, int V, typename T, typename GT, typename BT>
+__global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p) {
+  __shared__ Smem<K, V> sm;
+  __shared__ float xv_lds[K * 2];          // q and k after conv + SiLU
+  __shared__ float vv_lds[16][V];          // v heads of the group (R <= 16)
+  const int64_t b = blockIdx.x / p.H;
+  const int h = static_cast<int>(blockIdx.x % p.H);
+  const int R = p.HV / p.H;
+  const int tid = threadIdx.x;
+  const int64_t cslot = p.conv_idx ? p.conv_idx[b] : b;
+  const int64_t sslot = p.ssm_idx ? p.ssm_idx[b] : b;
+  if (p.conv_idx && cslot == p.pad) return;  // padded batch row
+
+  // Conv update for the group's channels: q (K), k (K), then R * V of v.
+  const int nch = 2 * K + R * V;
+  const bool conv_ok = cslot >= 0 && cslot < p.conv_lines;
+  for (int i = tid; i < nch; i += kThreads) {
+    int64_t ch;
+    if (i < K) ch = static_cast<int64_t>(h) * K + i;
+    else if (i < 2 * K) ch = static_cast<int64_t>(p.H) * K + static_cast<int64_t>(h) * K + (i - K);
+    else ch = 2 * static_cast<int64_t>(p.H) * K + static_cast<int64_t>(h) * R * V + (i - 2 * K);
+    const float xc = ldf<T>(p.x, b * p.sx + ch);
+    float acc = p.cbias ? load_as_f32(p.cbias, ch, p.wdt) : 0.f;
+    T* st = reinterpret_cast<T*>(p.conv_state) + cslot * p.cs_line + ch * p.cs_dim;
+    // window = cat(state[S-W+1 .. S-1], x)
+    for (int j = 0; j < p.W - 1; ++j) {
+      const float sv = conv_ok ? to_f32(st[(p.S - p.W + 1 + j) * p.cs_tok]) : 0.f;
+      acc = fmaf(sv, load_as_f32(p.w, ch * p.w_dim + j * p.w_tap, p.wdt), acc);
+    }
+    acc = fmaf(xc, load_as_f32(p.w, ch * p.w_dim + (p.W - 1) * p.w_tap, p.wdt), acc);
+    const float y = silu(acc);
+    if (conv_ok) {  // shift the state left by one and append x
+      for (int j = 0; j + 1 < p.S; ++j) st[j * p.cs_tok] = st[(j + 1) * p.cs_tok];
+      st[(p.S - 1) * p.cs_tok] = reinterpret_cast<const T*>(p.x)[b * p.sx + ch];
+    }
+    if (i < 2 * K) xv_lds[i] = y;
+    else vv_lds[(i - 2 * K) / V][(i - 2 * K) % V] = y;
+  }
+  __syncthreads();
+
+  const bool st_ok = sslot >= 0 && sslot < p.slots;
+  for (int j = 0; j < R; ++j) {
+    const int hv = h * R + j;
+    Tile<K, V> t;
+    float* sbase = p.state + sslot * p.st_slot_stride + static_cast<int64_t>(hv) * K * V;
+    if (st_ok) load_tile<K, V>(t, sbase); else zero_tile<K, V>(t);
+    prep_qk<K, V>(sm, [&](int which, int e) { return xv_lds[which * K + e]; },
+                  p.l2norm, p.scale);
+    if (tid < V) sm.v[tid] = vv_lds[j][tid];
+    const float decay = __expf(ldf<GT>(p.g, b * p.HV + hv));
+    const float beta = p.beta ? ldf<BT>(p.beta, b * p.HV + hv) : 1.0f;
+    T* o = reinterpret_cast<T*>(p.o) + (b * p.HV + hv) * V;
+    gdn_token<K, V>(t, sm, decay, beta, [&](int c, float val) { o[c] = from_f32<T>(val); });
+    if (st_ok) store_tile<K, V>(t, sbase);
+  }
+}
+
+template <int K, int V, typename T, typename GT>
+int fused_beta(const FusedParams& p, xk_dtype bdt, hipStream_t s) {
+  const dim3 grid(p.B * p.H);
+  switch (bdt) {
+    case XK_F32: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, float>), grid, dim3(kThreads), 0, s, p); break;
+    case XK_BF16: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, bf16>), grid, dim3(kThreads), 0, s, p); break;
+    case XK_F16: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, f16>), grid, dim3(kThreads), 0, s, p); break;
+    default: return XK_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+template <int K, int V, typename T>
+int fused_g(const FusedParams& p, xk_dtype gdt, xk_dtype bdt, hipStream_t s) {
+  switch (gdt) {
+    case XK_F32: return fused_beta<K, V, T, float>(p, bdt, s);
+    case XK_BF16: return fused_beta<K, V, T, bf16>(p, bdt, s);
+    case XK_F16: return fused_beta<K, V, T, f16>(p, bdt, s);
+    default: return XK_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace
+}  // namespace xk
+
+using namespace xk;
+
+extern "C" int xk_gdn_recurrent(
+    const void* q, const void* k, const void* v, xk_dtype dtype, const void* g,
+    xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype, void* o,
+    const float* initial_state, int64_t stride_h0_slot, float* final_state,
+    int64_t stride_ht_slot, int64_t num_slots, const void* cu_seqlens,
+    xk_dtype cu_dtype, const int32_t* ssm_state_indices, int64_t stride_idx_seq,
+    int64_t stride_idx_tok, const int32_t* num_accepted_tokens, int64_t N,
+    int64_t T, int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+    int use_qk_l2norm, int inplace_final_state, void* stream) {
+  if (N < 0 || T < 0 || H <= 0 || HV <= 0 || HV % H != 0) return XK_ERR_INVALID;
+  if (!is_float_dtype(dtype) || !is_float_dtype(g_dtype) ||
+      (beta && !is_float_dtype(beta_dtype)))
+    return XK_ERR_UNSUPPORTED;
+  if (cu_seqlens && cu_dtype != XK_I32 && cu_dtype != XK_I64) return XK_ERR_UNSUPPORTED;
+  if (N == 0) return XK_OK;
+  if (!q || !k || !v || !g || !o || !final_state) return XK_ERR_INVALID;
+  if (inplace_final_state && !ssm_state_indices) return XK_ERR_INVALID;
+  if (num_accepted_tokens && (!ssm_state_indices || !cu_seqlens || stride_idx_tok == 0))
+    return XK_ERR_INVALID;
+  if (!aligned(initial_state, 16) || !aligned(final_state, 16) ||
+      stride_h0_slot % 4 || stride_ht_slot % 4)
+    return XK_ERR_INVALID;
+  RecParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = g;
+  p.beta = beta;
+  p.o = o;
+  p.h0 = initial_state;
+  p.ht = final_state;
+  p.h0_slot_stride = stride_h0_slot;
+  p.ht_slot_stride = stride_ht_slot;
+  p.slots = num_slots;
+  p.cu = cu_seqlens;
+  p.cu_i64 = cu_dtype == XK_I64;
+  p.idx = ssm_state_indices;
+  p.idx_s0 = stride_idx_seq;
+  p.idx_s1 = stride_idx_tok;
+  p.accepted = num_accepted_tokens;
+  p.N = N;
+  p.T = T;
+  p.H = static_cast<int>(H);
+  p.HV = static_cast<int>(HV);
+  p.scale = scale;
+  p.l2norm = use_qk_l2norm;
+  p.inplace = inplace_final_state;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const xk_dtype bdt = beta ? beta_dtype : XK_F32;
+  if (K == 128 && V == 128) return rec_t<128, 128>(p, dtype, g_dtype, bdt, s);
+  if (K == 64 && V == 64) return rec_t<64, 64>(p, dtype, g_dtype, bdt, s);
+  if (K == 128 && V == 64) return rec_t<128, 64>(p, dtype, g_dtype, bdt, s);
+  if (K == 64 && V == 128) return rec_t<64, 128>(p, dtype, g_dtype, bdt, s);
+  return XK_ERR_UNSUPPORTED;
+}
+
+extern "C" int xk_gdn_conv_decode(
+    const void* mixed_qkv, int64_t stride_x_row, void* conv_state,
+    int64_t stride_cs_line, int64_t stride_cs_dim, int64_t stride_cs_tok,
+    int64_t conv_lines, int64_t conv_state_len, const void* conv_weight,
+    int64_t stride_w_dim, int64_t stride_w_tap, const void* conv_bias,
+    xk_dtype w_dtype, int64_t width, const int32_t* conv_state_indices,
+    int32_t pad_slot_id, const void* g, xk_dtype g_dtype, const void* beta,
+    xk_dtype beta_dtype, float* ssm_state, int64_t stride_state_slot,
+    int64_t num_slots, const int32_t* ssm_state_indices, void* o, int64_t B,
+    int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+    int use_qk_l2norm, xk_dtype dtype, void* stream) {
+  if (B < 0 || H <= 0 || HV <= 0 || HV % H != 0 || HV / H > 16 || width < 1 ||
+      conv_state_len < width - 1 || conv_state_len < 1)
+    return XK_ERR_INVALID;
+  if (!is_float_dtype(dtype) || !is_float_dtype(g_dtype) || !is_float_dtype(w_dtype) ||
+      (beta && !is_float_dtype(beta_dtype)))
+    return XK_ERR_UNSUPPORTED;
+  if (B == 0) return XK_OK;
+  if (!mixed_qkv || !conv_state || !conv_weight || !g || !ssm_state || !o)
+    return XK_ERR_INVALID;
+  if (!aligned(ssm_state, 16) || stride_state_slot % 4) return XK_ERR_INVALID;
+  FusedParams p{};
+  p.x = mixed_qkv;
+  p.sx = stride_x_row;
+  p.conv_state = conv_state;
+  p.cs_line = stride_cs_line;
+  p.cs_dim = stride_cs_dim;
+  p.cs_tok = stride_cs_tok;
+  p.conv_lines = conv_lines;
+  p.S = static_cast<int>(conv_state_len);
+  p.w = conv_weight;
+  p.w_dim = stride_w_dim;
+  p.w_tap = stride_w_tap;
+  p.cbias = conv_bias;
+  p.wdt = w_dtype;
+  p.conv_idx = conv_state_indices;
+  p.W = static_cast<int>(width);
+  p.g = g;
+  p.beta = beta;
+  p.state = ssm_state;
+  p.st_slot_stride = stride_state_slot;
+  p.slots = num_slots;
+  p.ssm_idx = ssm_state_indices;
+  p.o = o;
+  p.B = B;
+  p.H = static_cast<int>(H);
+  p.HV = static_cast<int>(HV);
+  p.scale = scale;
+  p.l2norm = use_qk_l2norm;
+  p.pad = pad_slot_id;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const xk_dtype bdt = beta ? beta_dtype : XK_F32;
+  if (K != 128 || V != 128) return XK_ERR_UNSUPPORTED;
+  switch (dtype) {
+    case XK_BF16: return fused_g<128, 128, bf16>(p, g_dtype, bdt, s);
+    case XK_F16: return fused_g<128, 128, f16>(p, g_dtype, bdt, s);
+    case XK_F32: return fused_g<128, 128, float>(p, g_dtype, bdt, s);
+    default: return XK_ERR_UNSUPPORTED;
+  }
+}

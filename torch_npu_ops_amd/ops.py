@@ -335,6 +335,99 @@ def npu_causal_conv1d_update_v2(x: torch.Tensor, conv_state: torch.Tensor,
     return out
 
 
+def npu_fused_recurrent_gated_delta_rule(
+        q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor,
+        beta: Optional[torch.Tensor] = None, scale: Optional[float] = None,
+        initial_state: Optional[torch.Tensor] = None,
+        inplace_final_state: bool = True,
+        cu_seqlens: Optional[torch.Tensor] = None,
+        ssm_state_indices: Optional[torch.Tensor] = None,
+        num_accepted_tokens: Optional[torch.Tensor] = None,
+        use_qk_l2norm_in_kernel: bool = True):
+    """Recurrent gated delta rule; returns (o, final_state).
+
+    Mirrors npu_fused_recurrent_gated_delta_rule
+    (triton_npu/torch_api/npu_triton_recurrent_gated_delta_rule.cpp:54-247):
+    q, k [B, T, H, K], v [B, T, HV, V], g / beta [B, T, HV]; B must be 1
+    unless cu_seqlens is given; o is [B, T, HV, V] (squeezed NK dim);
+    with inplace_final_state the returned state is initial_state itself.
+    The reference binaries ignore use_qk_l2norm_in_kernel (always on); here
+    it is honoured, with the compatibility default True.
+    """
+    B, T, H, K = k.shape
+    HV, V = v.shape[2], v.shape[3]
+    if cu_seqlens is None and q.size(0) != 1:
+        raise ValueError("batch size is not 1 when cu_seqlens is not provided")
+    if initial_state is None:
+        raise ValueError("initial_state must be provided")
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(K)
+    N = cu_seqlens.numel() - 1 if cu_seqlens is not None else B
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    gc = g.contiguous()
+    bc = beta.contiguous() if beta is not None else None
+    o = torch.empty(B, T, HV, V, dtype=q.dtype, device=q.device)
+    h0 = initial_state
+    if h0.dtype != torch.float32 or not h0.is_contiguous():
+        raise ValueError("initial_state must be contiguous float32")
+    if inplace_final_state:
+        final = h0
+    else:
+        final = torch.empty(N, HV, K, V, dtype=torch.float32, device=q.device)
+    idx, s0, s1 = None, 0, 0
+    if ssm_state_indices is not None:
+        idx = ssm_state_indices.to(torch.int32).contiguous()
+        s0 = idx.stride(0)
+        s1 = idx.stride(1) if idx.dim() == 2 else 0
+    acc = num_accepted_tokens.to(torch.int32).contiguous() if num_accepted_tokens is not None else None
+    cu = cu_seqlens.contiguous() if cu_seqlens is not None else None
+    st = lib().xk_gdn_recurrent(
+        qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), xk_dtype(qc), gc.data_ptr(),
+        xk_dtype(gc), _ptr(bc), xk_dtype(bc) if bc is not None else 0, o.data_ptr(),
+        h0.data_ptr(), h0.stride(0), final.data_ptr(), final.stride(0), h0.size(0),
+        _ptr(cu), xk_dtype(cu) if cu is not None else 0, _ptr(idx), s0, s1,
+        _ptr(acc), N, T if cu is None else 0, H, HV, K, V, sc,
+        int(use_qk_l2norm_in_kernel), int(inplace_final_state), _stream(q))
+    check(st, "xk_gdn_recurrent")
+    return o, final
+
+
+def gdn_conv_decode(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
+                    conv_weight: torch.Tensor, g: torch.Tensor,
+                    beta: Optional[torch.Tensor], ssm_state: torch.Tensor,
+                    num_heads_qk: int, num_heads_v: int, head_k: int = 128,
+                    head_v: int = 128, scale: Optional[float] = None,
+                    conv_bias: Optional[torch.Tensor] = None,
+                    conv_state_indices: Optional[torch.Tensor] = None,
+                    ssm_state_indices: Optional[torch.Tensor] = None,
+                    pad_slot_id: int = -1, use_qk_l2norm: bool = True):
+    """One fused decode step: conv1d update + SiLU of mixed_qkv [B, D],
+    split into q / k / v heads, l2norm, one gated-delta-rule step on
+    ssm_state (updated in place).  Returns o [B, HV, V]."""
+    B, D = mixed_qkv.shape
+    if D != 2 * num_heads_qk * head_k + num_heads_v * head_v:
+        raise ValueError("mixed_qkv width does not match the head layout")
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(head_k)
+    x = mixed_qkv if mixed_qkv.stride(1) == 1 else mixed_qkv.contiguous()
+    w = conv_weight
+    cb = conv_bias.to(w.dtype).contiguous() if conv_bias is not None else None
+    ci = conv_state_indices.to(torch.int32).contiguous() if conv_state_indices is not None else None
+    si = ssm_state_indices.to(torch.int32).contiguous() if ssm_state_indices is not None else None
+    gc = g.contiguous()
+    bc = beta.contiguous() if beta is not None else None
+    o = torch.empty(B, num_heads_v, head_v, dtype=x.dtype, device=x.device)
+    st = lib().xk_gdn_conv_decode(
+        x.data_ptr(), x.stride(0), conv_state.data_ptr(), conv_state.stride(0),
+        conv_state.stride(1), conv_state.stride(2), conv_state.size(0),
+        conv_state.size(2), w.data_ptr(), w.stride(0), w.stride(1), _ptr(cb),
+        xk_dtype(w), w.size(1), _ptr(ci), int(pad_slot_id), gc.data_ptr(),
+        xk_dtype(gc), _ptr(bc), xk_dtype(bc) if bc is not None else 0,
+        ssm_state.data_ptr(), ssm_state.stride(0), ssm_state.size(0), _ptr(si),
+        o.data_ptr(), B, num_heads_qk, num_heads_v, head_k, head_v, sc,
+        int(use_qk_l2norm), xk_dtype(x), _stream(x))
+    check(st, "xk_gdn_conv_decode")
+    return o
+
+
 def npu_l2norm_last_dim(x: torch.Tensor, eps: float = 1e-6,
                         output_dtype: Optional[torch.dtype] = None):
     """x * rsqrt(sum(x^2) + eps) over the last dim.
