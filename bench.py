@@ -29,6 +29,7 @@ import time
 import torch
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_TFS = 2500.0  # dense bf16
 ROTATE_BYTES = 1 << 30  # >= 1 GiB of distinct buffers per op
 MAX_SETS = 128
 CPU_THREADS = min(16, os.cpu_count() or 1)
@@ -160,14 +161,18 @@ class RopeCase(Case):
     algo_bytes = (T * (HQ + 2 * HKV) * HD * 4 * 2 + 2 * HD * 4 + 2 * T * HD * 4)
 
     def __init__(self):
-        from oracle import rope as orp
         g = torch.Generator().manual_seed(0)
         hid = (self.HQ + 2 * self.HKV) * self.HD
         self.qkv = _randn((self.T, hid), g, torch.float32)
         self.qw = _randn((self.HD,), g, torch.float32, 0.1, 1.0)
         self.kw = _randn((self.HD,), g, torch.float32, 0.1, 1.0)
         pos = torch.randint(0, 4096, (self.T,), generator=g)
-        self.cos, self.sin = orp.neox_cos_sin(pos, orp.inv_freq_table(self.HD, 1e6))
+        # neox rows: cos/sin of pos * theta^(-2i/HD), each half repeated.
+        i = torch.arange(0, self.HD, 2, dtype=torch.float64)
+        inv = (1.0 / (1e6 ** (i / self.HD))).to(torch.float32)
+        f = pos.to(torch.float32)[:, None] * inv[None, :]
+        self.cos = torch.cat([f.cos(), f.cos()], -1)
+        self.sin = torch.cat([f.sin(), f.sin()], -1)
 
     def sets(self, dev, n):
         from torch_npu_ops_amd import _lib
@@ -427,8 +432,81 @@ class GdnRecurrentCase(Case):
         return run, f"{n} of 256 sequences, fp32", a.B / n
 
 
+def chunk_gdn_flops(tokens, HV, K=128, V=128, C=64):
+    """Algorithmic FLOPs of the chunked gated delta rule per call, summed
+    per 64-token chunk and v-head: K K^T, Q K^T (2C^2K each), W = A(k b e^g)
+    (2C^2K), U = A(v b) and (QK^T) Vn (2C^2V each), W S, Q S and the state
+    update K^T Vn (2CKV each), and the triangular inverse (C^3/3)."""
+    per_chunk = 3 * 2 * C * C * K + 2 * 2 * C * C * V + 3 * 2 * C * K * V + C ** 3 // 3
+    return tokens * HV * per_chunk // C
+
+
+class GdnChunkCase(Case):
+    name = "gdn_chunk_prefill"
+    config = ("config 4: chunked gated delta rule prefill bf16, 8 sequences "
+              "(lengths U[512,3584], 16384 tokens), 16 qk / 32 v heads, head_dim "
+              "128, chunk 64, q/k l2-normalised, g=-softplus(N(0,1)) fp32, "
+              "beta=sigmoid(N(0,1)) bf16, h0~N(0,0.02) fp32, outputs o + final state")
+    kernel = "gdn_chunk_state_kernel"
+    T, NSEQ, H, HV, K, V = 16384, 8, 16, 32, 128, 128
+    # q/k + v + o (bf16) + g (fp32) + beta (bf16) + h0/ht (fp32)
+    algo_bytes = (T * H * K * 2 * 2 + T * HV * V * 2 * 2 + T * HV * (4 + 2)
+                  + NSEQ * HV * K * V * 4 * 2)
+    algo_flops = chunk_gdn_flops(T, HV, K, V)
+    tokens = T
+
+    def __init__(self):
+        import torch.nn.functional as F
+        g = torch.Generator().manual_seed(0)
+        lens = varlen_lengths(self.NSEQ, self.T, 512, 3584, g)
+        self.cu = torch.zeros(self.NSEQ + 1, dtype=torch.int32)
+        self.cu[1:] = torch.cumsum(lens, 0)
+
+        def unit(x):
+            return (x * torch.rsqrt((x * x).sum(-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+        self.q = unit(torch.randn(self.T, self.H, self.K, generator=g))
+        self.k = unit(torch.randn(self.T, self.H, self.K, generator=g))
+        self.v = _randn((self.T, self.HV, self.V), g, torch.bfloat16)
+        self.g = -F.softplus(torch.randn(self.T, self.HV, generator=g))
+        self.beta = torch.sigmoid(torch.randn(self.T, self.HV, generator=g)).to(torch.bfloat16)
+        self.h0 = torch.randn(self.NSEQ, self.HV, self.K, self.V, generator=g) * 0.02
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        cu = self.cu.to(dev)
+        wsb = lib.xk_gdn_chunk_workspace_bytes(self.T, self.NSEQ, self.HV)
+        out = []
+        for _ in range(n):
+            q, k, v = self.q.to(dev), self.k.to(dev), self.v.to(dev)
+            g, beta, h0 = self.g.to(dev), self.beta.to(dev), self.h0.to(dev)
+            o = torch.empty_like(v)
+            ht = torch.empty_like(h0)
+            ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+
+            def run(q=q, k=k, v=v, g=g, beta=beta, h0=h0, o=o, ht=ht, ws=ws):
+                _ok(lib.xk_gdn_chunk_fwd(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.XK_BF16,
+                    g.data_ptr(), _lib.XK_F32, beta.data_ptr(), _lib.XK_BF16,
+                    o.data_ptr(), h0.data_ptr(), ht.data_ptr(), cu.data_ptr(),
+                    _lib.XK_I32, self.NSEQ, self.T, self.H, self.HV, self.K,
+                    self.V, self.K ** -0.5, 0, ws.data_ptr(), wsb, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import gdn as og
+        heads = list(range(0, self.HV, 4))  # bounded sample: 8 of 32 v-heads
+        a = (self.q[None], self.k[None], self.v[None], self.g[None], self.beta[None],
+             self.K ** -0.5, self.h0, self.cu)
+        return (lambda: og.chunk_gdn(*a, heads=heads),
+                f"all 16384 tokens, {len(heads)} of {self.HV} v-heads, fp32 "
+                "chunked form of the reference golden", self.HV / len(heads))
+
+
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
-                             ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase)}
+                             ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase,
+                             GdnChunkCase)}
 HEADLINE = "layer_norm_fwd"
 
 
@@ -528,18 +606,46 @@ def main():
                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
                          "frac": round(gbs / HBM_PEAK_GBS, 4)},
         }
+        flops = getattr(case, "algo_flops", 0)
+        if flops:
+            tfs = flops / (ms * 1e-3) / 1e12
+            ops[name]["tokens/s"] = round(case.tokens / (ms * 1e-3))
+            ops[name]["algo_flops"] = flops
+            ops[name]["mfma_roofline"] = {
+                "bound": "mfma", "achieved": round(tfs, 2), "peak": MFMA_BF16_TFS,
+                "unit": "TFLOP/s", "frac": round(tfs / MFMA_BF16_TFS, 4)}
+            # Which floor is higher: HBM bytes at 8 TB/s or FLOPs at 2.5 PFLOP/s.
+            t_hbm = case.algo_bytes / (HBM_PEAK_GBS * 1e9)
+            t_mfma = flops / (MFMA_BF16_TFS * 1e12)
+            ops[name]["bound"] = "hbm" if t_hbm >= t_mfma else "mfma"
+            ops[name]["frac_of_bound"] = round(max(t_hbm, t_mfma) / (ms * 1e-3), 4)
         print(f"[bench] {name}: {ms*1e3:.2f} us/call, {gbs:.0f} GB/s "
-              f"({gbs / HBM_PEAK_GBS:.1%} of peak)", file=sys.stderr, flush=True)
+              f"({gbs / HBM_PEAK_GBS:.1%} of peak)"
+              + (f", {ops[name]['tokens/s']:.3g} tokens/s, "
+                 f"{ops[name]['mfma_roofline']['achieved']} TFLOP/s" if flops else ""),
+              file=sys.stderr, flush=True)
     head = ops[headline]
     case = CASES[headline]()
     cpu = None
     if not args.no_cpu:
         sec, sample, nrun = time_cpu(case)
-        cpu = {"value": round(case.algo_bytes / sec / 1e9, 2), "unit": "GB/s",
+        per_tok = getattr(case, "tokens", 0)
+        cpu = {"value": round(per_tok / sec) if per_tok else round(case.algo_bytes / sec / 1e9, 2),
+               "unit": "tokens/s" if per_tok else "GB/s",
                "cores": CPU_THREADS, "kind": "port",
                "sample": f"{sample}; median of {nrun} runs, {sec*1e3:.1f} ms/call"}
         print(f"[bench] cpu baseline {headline}: {sec*1e3:.1f} ms/call",
               file=sys.stderr, flush=True)
+        # The chunked prefill's target is stated against its CPU tokens/s.
+        if GdnChunkCase.name in ops and headline != GdnChunkCase.name:
+            csec, csample, cn = time_cpu(GdnChunkCase())
+            ops[GdnChunkCase.name]["cpu_baseline"] = {
+                "value": round(GdnChunkCase.tokens / csec), "unit": "tokens/s",
+                "cores": CPU_THREADS, "kind": "port",
+                "sample": f"{csample}; median of {cn} runs, scaled to the full "
+                          f"config: {csec*1e3:.0f} ms/call"}
+            print(f"[bench] cpu baseline {GdnChunkCase.name}: {csec*1e3:.0f} ms/call",
+                  file=sys.stderr, flush=True)
     line = {
         "metric": "achieved HBM GB/s (% of peak) per op; chunked GDN prefill tokens/s",
         "value": head["GB/s"],

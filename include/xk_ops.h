@@ -224,6 +224,32 @@ int xk_gdn_conv_decode(
     int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
     int use_qk_l2norm, xk_dtype dtype, void* stream);
 
+/* ------------------------------------------------------------------------
+ * a6. Chunked gated delta rule (prefill), chunk size 64.
+ * Replaces xllm::kernel::npu::npu_chunk_gated_delta_rule
+ *   (triton_npu/torch_api/triton_ops_api.h:111-122,
+ *    npu_triton_chunk_gated_delta_rule.cpp:556-642) -- the whole pipeline
+ * of cumsum, scaled K K^T, solve_tril, WY recompute, state recurrence and
+ * output (a6b-a6g) in three launches with no host synchronisation.
+ *   q, k : [total_tokens, H, K]; v, o : [total_tokens, HV, V] (dtype
+ *   bf16, as the reference requires); g : [total_tokens, HV] log-decay,
+ *   beta : [total_tokens, HV] (each fp32 or bf16); sequences cu_seqlens[n]..cu_seqlens[n+1] (int32 or
+ *   int64, device).  initial_state / final_state : fp32 [N, HV, K, V] (NULL
+ *   = zero / not written).  use_qk_l2norm applies x / sqrt(sum x^2 + 1e-6)
+ *   to q and k first.  K = 128, V a multiple of 32.
+ *   workspace >= xk_gdn_chunk_workspace_bytes(total_tokens, N, HV) bytes,
+ *   256-byte aligned (chunk offsets + per-chunk inverse blocks).
+ */
+int64_t xk_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t num_seqs,
+                                     int64_t HV);
+int xk_gdn_chunk_fwd(
+    const void* q, const void* k, const void* v, xk_dtype dtype, const void* g,
+    xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype, void* o,
+    const float* initial_state, float* final_state, const void* cu_seqlens,
+    xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
+    int64_t K, int64_t V, float scale, int use_qk_l2norm, void* workspace,
+    size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

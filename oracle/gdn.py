@@ -127,26 +127,34 @@ def chunk_gdn(q, k, v, g, beta, scale: Optional[float], initial_state,
     bounds = _bounds(cu_seqlens, 1, T)
     o = torch.zeros(T, HV, V, dtype=dtype)
     fin = torch.zeros(len(bounds), HV, K, V, dtype=dtype)
+    hs = list(range(HV)) if heads is None else list(heads)
+    hi = torch.tensor(hs)
+    # The golden loops over heads one at a time; the same per-head algebra
+    # is batched over the head dimension here (matmuls per head, the row
+    # recurrence stepped for all heads together).
     for n, (a, b) in enumerate(bounds):
-        for h in (range(HV) if heads is None else heads):
-            S = (initial_state[n, h].to(dtype).clone() if initial_state is not None
-                 else torch.zeros(K, V, dtype=dtype))
-            for s in range(a, b, chunk):
-                e = min(s + chunk, b)
-                L = e - s
-                qc = qf[s:e, h] * scale
-                kc, vc, bc, gcc = kf[s:e, h], vf[s:e, h], bf[s:e, h], gc[s:e, h]
-                decay = torch.tril(torch.exp(gcc[:, None] - gcc[None, :]))
-                A = torch.tril(-(kc * bc[:, None]) @ kc.t() * decay, -1)
-                for r in range(1, L):  # row recurrence, test.cpp:251-257
-                    A[r, :r] = A[r, :r] + A[r, :r] @ A[:r, :r]
-                A = A + torch.eye(L, dtype=dtype)
-                u = A @ (vc * bc[:, None])
-                w = A @ (kc * bc[:, None] * torch.exp(gcc)[:, None])
-                attn = torch.tril(qc @ kc.t() * decay)
-                vn = u - w @ S
-                o[s:e, h] = (qc * torch.exp(gcc)[:, None]) @ S + attn @ vn
-                gl = gcc[L - 1]
-                S = S * torch.exp(gl) + (kc * torch.exp(gl - gcc)[:, None]).t() @ vn
-            fin[n, h] = S
+        S = (initial_state[n, hi].to(dtype).clone() if initial_state is not None
+             else torch.zeros(len(hs), K, V, dtype=dtype))
+        for s in range(a, b, chunk):
+            e = min(s + chunk, b)
+            L = e - s
+            qc = qf[s:e, hi].transpose(0, 1) * scale                 # [h, L, K]
+            kc = kf[s:e, hi].transpose(0, 1)
+            vc = vf[s:e, hi].transpose(0, 1)                         # [h, L, V]
+            bc = bf[s:e, hi].transpose(0, 1)                         # [h, L]
+            gcc = gc[s:e, hi].transpose(0, 1)
+            decay = torch.tril(torch.exp(gcc[:, :, None] - gcc[:, None, :]))
+            A = torch.tril(-((kc * bc[..., None]) @ kc.transpose(1, 2)) * decay, -1)
+            for r in range(1, L):  # row recurrence, test.cpp:251-257
+                A[:, r, :r] = A[:, r, :r] + (A[:, r:r + 1, :r] @ A[:, :r, :r])[:, 0]
+            A = A + torch.eye(L, dtype=dtype)
+            u = A @ (vc * bc[..., None])
+            w = A @ (kc * bc[..., None] * torch.exp(gcc)[..., None])
+            attn = torch.tril(qc @ kc.transpose(1, 2) * decay)
+            vn = u - w @ S
+            o[s:e, hi] = ((qc * torch.exp(gcc)[..., None]) @ S + attn @ vn).transpose(0, 1)
+            gl = gcc[:, L - 1]
+            S = (S * torch.exp(gl)[:, None, None]
+                 + (kc * torch.exp(gl[:, None] - gcc)[..., None]).transpose(1, 2) @ vn)
+        fin[n, hi] = S
     return o.unsqueeze(0), fin

@@ -1,0 +1,844 @@
+// Chunked gated delta rule (prefill) for gfx950, chunk size 64.
+//
+// Semantics follow chunk_gated_delta_rule_full_op_ref
+// (triton_npu/test/triton_chunk_gated_delta_rule_test.cpp:190-323), the
+// pipeline of triton_npu/triton_src/chunk_gated_delta_rule/chunk.py:32-80.
+// Per sequence, per v-head, per 64-token chunk with in-chunk cumulative
+// log-decay gc (cumsum.py), beta b, keys k, queries q (scaled), values v and
+// carried state S [K, V] (fp32):
+//   M    = strict_tril(b_i (k_i . k_j) exp(gc_i - gc_j))     (kkt.py)
+//   Ai   = (I + M)^-1                                        (solve_tril.py)
+//   Vn   = Ai (b * (v - exp(gc) * (k S)))     == u - w S      (wy_fast.py,
+//                                                            chunk_delta_h.py)
+//   o    = exp(gc) * (q S) + tril(q k^T * exp(gc_i - gc_j)) Vn (chunk_o.py)
+//   S   <- exp(gc_last) S + k^T (exp(gc_last - gc) * Vn)
+// GQA: v-head hv uses qk-head hv / (HV / H).  Optional l2norm of q and k
+// (npu_l2norm_last_dim, x / sqrt(sum x^2 + 1e-6)) is folded in as per-token
+// row scales, so the matrix products always see the exact bf16 inputs.
+//
+// Three launches, no host synchronisation (capturable in a hipGraph):
+//  * P0 (one small block) turns cu_seqlens into chunk offsets.
+//  * P1, fully parallel, one wave per (chunk, v-head), computes everything
+//    that does not depend on the carried state and writes one record per
+//    (chunk, head) to the workspace:
+//      - Ai = (I + M)^-1 as a bf16 hi/lo pair (hi + lo carries ~16 mantissa
+//        bits).  K K^T runs on bf16 MFMA (exact products, fp32 sums); the
+//        inverse inverts the two 32x32 diagonal blocks by forward
+//        substitution (one lane per column) and forms the off-diagonal block
+//        X10 = -X11 M10 X00 with hi/lo-split MFMAs;
+//      - Aq = scale * tril(r_q r_k (q k^T) exp(gc_i - gc_j)) in bf16 (it only
+//        feeds the bf16 output);
+//      - per-token factors cq = scale exp(gc) r_q, ck = b exp(gc) r_k, b,
+//        ed = r_k exp(gc_last - gc), and exp(gc_last).
+//  * P2, sequential over the chunks of a sequence, one 256-lane block per
+//    (sequence, v-head, 32-column V tile), carries the fp32 state tile in LDS
+//    through the short dependent chain
+//      KS = K S -> R = b v - ck KS -> Vn = Ai R -> S = e^gl S + K^T (ed Vn)
+//    (hi/lo-split bf16 MFMAs keep the state within fp32-reference tolerance)
+//    and emits o = cq (Q S) + Aq Vn.  Every global operand of chunk c+1 is
+//    loaded into registers while chunk c computes, so the chain never waits
+//    on HBM.  Blocks of one (sequence, head) share an XCD (block id mod 8)
+//    and thus its L2 for the shared q/k/record reads.
+#include "xk_common.h"
+
+namespace xk {
+namespace {
+
+constexpr int kC = 64;    // chunk size
+constexpr int kBV = 32;   // V columns per P2 block
+constexpr int kTh = 256;  // threads per block
+// Per-(chunk, head) record: ai_hi, ai_lo, aq (bf16 [64][64] each), then the
+// per-token factors (fp32 [5][64]: cq, ck, b, ed, exp(gc_last)).
+constexpr int kMat = kC * kC * 2;
+constexpr int kRec = 3 * kMat + 5 * kC * 4;  // 25856 = 101 * 256
+static_assert(kRec % 256 == 0, "records stay 256-byte aligned");
+// Padded rows of a sequence's last chunk store their (unused) outputs here,
+// so that every store in the chunk loop is unconditional: gfx9 counts loads
+// and stores in one in-order counter, and a store that only some paths
+// issue makes the compiler wait for every outstanding prefetch.
+constexpr int kDump = kC * kBV * 2;
+
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4_t mfma16(const bf8_t& a, const bf8_t& b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi).
+__device__ __forceinline__ void split(float x, __bf16& hi, __bf16& lo) {
+  hi = static_cast<__bf16>(x);
+  lo = static_cast<__bf16>(x - static_cast<float>(hi));
+}
+
+// Eight consecutive fp32 values (16-byte aligned) split into hi / lo.
+__device__ __forceinline__ void split8(const float* p, bf8_t& h, bf8_t& l) {
+  const f4_t a = *reinterpret_cast<const f4_t*>(p);
+  const f4_t b = *reinterpret_cast<const f4_t*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    __bf16 x, y;
+    split(a[e], x, y);
+    h[e] = x;
+    l[e] = y;
+    split(b[e], x, y);
+    h[e + 4] = x;
+    l[e + 4] = y;
+  }
+}
+
+__device__ __forceinline__ f4_t mfma_split3(const bf8_t& ah, const bf8_t& al, const bf8_t& bh,
+                                            const bf8_t& bl, f4_t c) {
+  c = mfma16(ah, bh, c);
+  c = mfma16(ah, bl, c);
+  return mfma16(al, bh, c);
+}
+
+template <typename T>
+__device__ __forceinline__ float ldf(const void* p, int64_t i) {
+  return to_f32(reinterpret_cast<const T*>(p)[i]);
+}
+
+struct ChunkParams {
+  const void* q;  // [T, H, K]
+  const void* k;
+  const void* v;  // [T, HV, V]
+  const void* g;  // [T, HV]
+  const void* beta;
+  void* o;  // [T, HV, V]
+  const float* h0;  // [N, HV, K, V] or NULL
+  float* ht;        // [N, HV, K, V] or NULL
+  const void* cu;   // [N+1]
+  int cu_i64;
+  int32_t* chunk_off;  // [N+1] workspace
+  bf16* dump;          // [64 * 32] workspace: sink for padded-row stores
+  char* rec;           // [NTmax, HV] records of kRec bytes, workspace
+  int64_t N, NTmax;
+  int64_t T;  // token rows of q/k/v
+  int H, HV;
+  float scale;
+  int l2norm;
+};
+
+// cu_seqlens[i], clamped to [0, T] so that a malformed table can never
+// index past the token rows (or the workspace sized from T).
+__device__ __forceinline__ int64_t cu_at(const ChunkParams& p, int64_t i) {
+  const int64_t v = p.cu_i64 ? reinterpret_cast<const int64_t*>(p.cu)[i]
+                             : static_cast<int64_t>(reinterpret_cast<const int32_t*>(p.cu)[i]);
+  return min(max(v, int64_t{0}), p.T);
+}
+
+__device__ __forceinline__ char* rec_at(const ChunkParams& p, int64_t c, int hv) {
+  return p.rec + (c * p.HV + hv) * static_cast<int64_t>(kRec);
+}
+
+// P0: chunk_off[n] = sum_{m<n} ceil(len_m / 64).  One block.
+__global__ void __launch_bounds__(kTh) gdn_chunk_offsets_kernel(ChunkParams p) {
+  __shared__ int32_t part[kTh];
+  const int tid = threadIdx.x;
+  const int64_t per = (p.N + kTh - 1) / kTh;
+  const int64_t b0 = tid * per, b1 = min(p.N, b0 + per);
+  int32_t s = 0;
+  for (int64_t n = b0; n < b1; ++n) {
+    const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
+    s += static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+  }
+  part[tid] = s;
+  __syncthreads();
+  if (tid == 0) {
+    int32_t acc = 0;
+    for (int i = 0; i < kTh; ++i) {
+      const int32_t v = part[i];
+      part[i] = acc;
+      acc += v;
+    }
+  }
+  __syncthreads();
+  int32_t acc = part[tid];
+  for (int64_t n = b0; n < b1; ++n) {
+    p.chunk_off[n] = acc;
+    const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
+    acc += static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+  }
+  if (tid == kTh - 1) p.chunk_off[p.N] = acc;
+}
+
+// Locates global chunk c: sequence n, token start s, length L (<= 64).
+// Returns false if c is past the last chunk.
+__device__ __forceinline__ bool locate_chunk(const ChunkParams& p, int64_t c, int64_t& n,
+                                             int64_t& s, int& L) {
+  if (c >= p.chunk_off[p.N]) return false;
+  int64_t lo = 0, hi = p.N;  // chunk_off[lo] <= c < chunk_off[hi]
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (p.chunk_off[mid] <= c) lo = mid; else hi = mid;
+  }
+  n = lo;
+  const int64_t ci = c - p.chunk_off[n];
+  const int64_t a = cu_at(p, n), b = cu_at(p, n + 1);
+  s = a + ci * kC;
+  L = static_cast<int>(min<int64_t>(kC, b - s));
+  return true;
+}
+
+// Lane's MFMA operand of a 16-row slab of a [64 tokens x K] matrix in global
+// memory (token t of the slab at element (row0 + t) * row_stride + col_off):
+// row = r0 + (lane & 15), 8 elements from kk*32 + 8*(lane>>4).  Rows >= L
+// repeat row L-1 of the same chunk (branch-free, so the load never stalls
+// the wave); every consumer zeroes those rows through factors that are 0
+// there (beta, ck, ed, the masks of M and Aq).
+__device__ __forceinline__ bf8_t load_rows_op(const void* base, int64_t col_off, int64_t row0,
+                                              int L, int64_t row_stride, int r0, int kk) {
+  const int lane = threadIdx.x & 63;
+  const int r = min(r0 + (lane & 15), L - 1);
+  const bf16* src = reinterpret_cast<const bf16*>(base) + (row0 + r) * row_stride + col_off +
+                    kk * 32 + 8 * (lane >> 4);
+  return *reinterpret_cast<const bf8_t*>(src);
+}
+
+// ---------------------------------------------------------------------------
+// P1: one wave per (chunk, v-head); waves of a block are independent.
+// ---------------------------------------------------------------------------
+constexpr int kLd = kC + 4;  // fp32 LDS row stride: rows stay 16-byte aligned
+
+template <int K, typename GT, typename BT>
+__global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
+  __shared__ __align__(16) float lds[4][kC][kLd];
+  __shared__ float vec[4][4][kC];  // gc, beta, r_k, r_q per wave
+  const int wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  const int64_t c = blockIdx.x;
+  const int hv = blockIdx.y * 4 + wid;
+  int64_t n, s;
+  int L;
+  // Wave-uniform exit; the kernel has no block-level barriers.
+  if (!(hv < p.HV && locate_chunk(p, c, n, s, L))) return;
+  float (*X)[kLd] = lds[wid];
+  float* gcv = vec[wid][0];
+  float* btv = vec[wid][1];
+  float* rkv = vec[wid][2];
+  float* rqv = vec[wid][3];
+  const int hq = hv / (p.HV / p.H);
+  constexpr int KK = K / 32;
+  const int64_t rs = static_cast<int64_t>(p.H) * K;
+
+  // K rows of the chunk as MFMA operands (A and B^T read the same rows).
+  bf8_t kop[4][KK];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      kop[mi][kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
+  // Per-token g (inclusive scan within the chunk) and beta; padded rows 0
+  // (loads clamped to row L-1, then selected away).
+  const int lt = min(lane, L - 1);
+  const float graw = ldf<GT>(p.g, (s + lt) * p.HV + hv);
+  const float braw = ldf<BT>(p.beta, (s + lt) * p.HV + hv);
+  float gv = lane < L ? graw : 0.f;
+  const float bv = lane < L ? braw : 0.f;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const float t = __shfl_up(gv, o, kWave);
+    if (lane >= o) gv += t;
+  }
+  gcv[lane] = gv;
+  btv[lane] = bv;
+  // Row scales r = 1 / sqrt(sum x^2 + 1e-6) of the rows this lane holds
+  // (row mi*16 + l15; the four lg lanes hold its four 32-wide pieces).
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    float ss = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = static_cast<float>(kop[mi][kk][e]);
+        ss = fmaf(x, x, ss);
+      }
+    ss += __shfl_xor(ss, 16, kWave);
+    ss += __shfl_xor(ss, 32, kWave);
+    if (lg == 0) rkv[mi * 16 + l15] = p.l2norm ? 1.0f / sqrtf(ss + 1e-6f) : 1.0f;
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  // M = strict_tril(b_i r_i r_j (k_i . k_j) exp(gc_i - gc_j)) into X (the
+  // ten lower 16x16 tiles; the strictly upper ones are never read).
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int nj = 0; nj <= mi; ++nj) {
+      f4_t a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) a = mfma16(kop[mi][kk], kop[nj][kk], a);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = mi * 16 + 4 * lg + i, col = nj * 16 + l15;
+        float m = 0.f;
+        if (row > col)
+          m = btv[row] * rkv[row] * rkv[col] * a[i] * __expf(gcv[row] - gcv[col]);
+        X[row][col] = m;
+      }
+    }
+  __builtin_amdgcn_wave_barrier();
+
+  // Diagonal blocks: lane (b, cc) forms column cc of X_bb = (I + M_bb)^-1,
+  //   x[i] = delta_{i,cc} - sum_{j<i} M_bb[i][j] x[j].
+  const int b = lane >> 5, cc = lane & 31, base = b * 32;
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float* mr = &X[base + i][base];
+    float a0 = (i == cc) ? 1.f : 0.f, a1 = 0.f;
+#pragma unroll
+    for (int j = 0; j + 1 < i; j += 2) {
+      a0 = fmaf(-mr[j], x[j], a0);
+      a1 = fmaf(-mr[j + 1], x[j + 1], a1);
+    }
+    if (i & 1) a0 = fmaf(-mr[i - 1], x[i - 1], a0);
+    x[i] = a0 + a1;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // X_00 transposed into the (spent) M_00 block, X_11 row-major into M_11.
+  if (b == 0) {
+#pragma unroll
+    for (int i = 0; i < 32; i += 4)
+      *reinterpret_cast<f4_t*>(&X[cc][i]) = f4_t{x[i], x[i + 1], x[i + 2], x[i + 3]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) X[32 + i][32 + cc] = x[i];
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  // T = M_10 X_00 (32 x 32), hi/lo-split operands.
+  f4_t tt[2][2];
+  {
+    bf8_t bh[2], bl[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) split8(&X[nt * 16 + l15][8 * lg], bh[nt], bl[nt]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      bf8_t ah, al;
+      split8(&X[32 + mt * 16 + l15][8 * lg], ah, al);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        tt[mt][nt] = mfma_split3(ah, al, bh[nt], bl[nt], f4_t{0.f, 0.f, 0.f, 0.f});
+    }
+  }
+  // T transposed into the unused upper-right block: X[n][32 + k] = T[k][n].
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+      *reinterpret_cast<f4_t*>(&X[nt * 16 + l15][32 + mt * 16 + 4 * lg]) = tt[mt][nt];
+  __builtin_amdgcn_wave_barrier();
+  // X_10 = -X_11 T.
+  f4_t x10[2][2];
+  {
+    bf8_t bh[2], bl[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) split8(&X[nt * 16 + l15][32 + 8 * lg], bh[nt], bl[nt]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      bf8_t ah, al;
+      split8(&X[32 + mt * 16 + l15][32 + 8 * lg], ah, al);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        x10[mt][nt] = mfma_split3(ah, al, bh[nt], bl[nt], f4_t{0.f, 0.f, 0.f, 0.f});
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  // Assemble X = (I + M)^-1 row-major: X_10 over M_10, X_00 row-major over
+  // its transpose, zeros over T.
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) X[32 + mt * 16 + 4 * lg + i][nt * 16 + l15] = -x10[mt][nt][i];
+  if (b == 0) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      X[i][cc] = x[i];
+      X[i][32 + cc] = 0.f;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  char* rec = rec_at(p, c, hv);
+  __bf16* aih = reinterpret_cast<__bf16*>(rec);
+  __bf16* ail = reinterpret_cast<__bf16*>(rec + kMat);
+  __bf16* aqp = reinterpret_cast<__bf16*>(rec + 2 * kMat);
+  float* sc = reinterpret_cast<float*>(rec + 3 * kMat);
+  // Lane r stores row r of Ai as hi and lo bf16 rows.
+#pragma unroll
+  for (int j0 = 0; j0 < kC; j0 += 8) {
+    bf8_t h, l;
+    split8(&X[lane][j0], h, l);
+    *reinterpret_cast<bf8_t*>(aih + lane * kC + j0) = h;
+    *reinterpret_cast<bf8_t*>(ail + lane * kC + j0) = l;
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  // Aq = scale * tril(r_q r_k (q k^T) exp(gc_i - gc_j)), rows < L.
+  bf8_t qop[4][KK];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      qop[mi][kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    float ss = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float y = static_cast<float>(qop[mi][kk][e]);
+        ss = fmaf(y, y, ss);
+      }
+    ss += __shfl_xor(ss, 16, kWave);
+    ss += __shfl_xor(ss, 32, kWave);
+    if (lg == 0) rqv[mi * 16 + l15] = p.l2norm ? 1.0f / sqrtf(ss + 1e-6f) : 1.0f;
+  }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 4; ++nj) {
+      f4_t a = {0.f, 0.f, 0.f, 0.f};
+      if (nj <= mi) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) a = mfma16(qop[mi][kk], kop[nj][kk], a);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = mi * 16 + 4 * lg + i, col = nj * 16 + l15;
+        float val = 0.f;
+        if (nj <= mi && row >= col && row < L)
+          val = p.scale * rqv[row] * rkv[col] * a[i] * __expf(gcv[row] - gcv[col]);
+        X[row][col] = val;
+      }
+    }
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int j0 = 0; j0 < kC; j0 += 8) {
+    bf8_t h;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = static_cast<__bf16>(X[lane][j0 + e]);
+    *reinterpret_cast<bf8_t*>(aqp + lane * kC + j0) = h;
+  }
+
+  // Per-token factors (lane = token); rows >= L are zero.
+  const float gl = __shfl(gv, L - 1, kWave);
+  const bool in = lane < L;
+  const float eg = __expf(gv);
+  sc[0 * kC + lane] = in ? p.scale * eg * rqv[lane] : 0.f;
+  sc[1 * kC + lane] = in ? bv * eg * rkv[lane] : 0.f;
+  sc[2 * kC + lane] = bv;
+  sc[3 * kC + lane] = in ? rkv[lane] * __expf(gl - gv) : 0.f;
+  sc[4 * kC + lane] = __expf(gl);
+}
+
+// ---------------------------------------------------------------------------
+// P2: sequential chunk loop per (sequence, v-head, 32-column V tile).
+// ---------------------------------------------------------------------------
+constexpr int kLt = kC + 8;  // bf16 LDS row stride (144 B: 16-byte aligned)
+
+// The fp32 state tile itself lives in registers (each wave owns K/4 of its
+// rows, in MFMA C layout); LDS holds its bf16 hi / lo copy, the B operand of
+// K S, refreshed once per chunk.
+template <int K>
+struct __align__(16) P2Smem {
+  __bf16 sb[2][kBV][K + 8];   // state hi / lo, transposed: sb[h][v][k]
+  __bf16 kt[2][K][kLt];       // chunk keys transposed, double-buffered
+  __bf16 rt[2][kBV][kLt];     // R transposed, hi / lo
+  __bf16 vt[kBV][kLt];        // Vn transposed (bf16, for the output)
+  __bf16 dt[2][kBV][kLt];     // (ed * Vn) transposed, hi / lo
+};
+
+// Operands one lane reads from global memory for one chunk, in two groups:
+// those the chunk consumes first (double-buffered: loaded a whole chunk
+// ahead) and those it consumes late (one buffer, reloaded for the next chunk
+// once the current one is done with them), which keeps two waves per SIMD.
+template <int KK>
+struct EarlyOps {
+  bf8_t kA[KK];          // K rows wid*16 + l15 (A operands)
+  bf16 v[2][4];          // v at the lane's C-layout positions (raw: converting
+                         // at load time would stall on the load)
+  f4_t ck, bt;           // factors of rows wid*16 + 4*lg + i
+};
+template <int KK>
+struct LateOps {
+  bf8_t qA[KK];          // Q rows wid*16 + l15 (Q S only feeds the output)
+  bf8_t aiH[2], aiL[2];  // Ai rows wid*16 + l15, hi / lo
+  bf8_t aq[2];           // Aq rows wid*16 + l15
+  f4_t cq, ed;
+  float egl;             // exp(gc_last)
+};
+
+// Token row of q/k/v for C-layout row `r` (rows >= L read row L-1: finite,
+// and zeroed by their factors).
+__device__ __forceinline__ uint64_t tok_row(int64_t s, int r, int L) {
+  return static_cast<uint64_t>(s + min(r, L - 1));
+}
+
+template <int K>
+__device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32>& ops,
+                                           int64_t s, int L, int64_t cidx, int hv, int hq,
+                                           uint32_t vrow, int vcol0) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int l15 = lane & 15, lg = lane >> 4;
+  const uint32_t rs = static_cast<uint32_t>(p.H) * K;
+  const bf16* kp = reinterpret_cast<const bf16*>(p.k) + tok_row(s, wid * 16 + l15, L) * rs +
+                   hq * K + 8 * lg;
+#pragma unroll
+  for (int kk = 0; kk < K / 32; ++kk) ops.kA[kk] = *reinterpret_cast<const bf8_t*>(kp + kk * 32);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bf16* vp = reinterpret_cast<const bf16*>(p.v) +
+                     tok_row(s, wid * 16 + 4 * lg + i, L) * vrow + vcol0 + l15;
+    ops.v[0][i] = vp[0];
+    ops.v[1][i] = vp[16];
+  }
+  const float* sc = reinterpret_cast<const float*>(rec_at(p, cidx, hv) + 3 * kMat);
+  const int r4 = wid * 16 + 4 * lg;
+  ops.ck = *reinterpret_cast<const f4_t*>(sc + 1 * kC + r4);
+  ops.bt = *reinterpret_cast<const f4_t*>(sc + 2 * kC + r4);
+}
+
+template <int K>
+__device__ __forceinline__ void load_late(const ChunkParams& p, LateOps<K / 32>& ops,
+                                          int64_t s, int L, int64_t cidx, int hv, int hq) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int l15 = lane & 15, lg = lane >> 4;
+  const uint32_t rs = static_cast<uint32_t>(p.H) * K;
+  const bf16* qp = reinterpret_cast<const bf16*>(p.q) + tok_row(s, wid * 16 + l15, L) * rs +
+                   hq * K + 8 * lg;
+#pragma unroll
+  for (int kk = 0; kk < K / 32; ++kk) ops.qA[kk] = *reinterpret_cast<const bf8_t*>(qp + kk * 32);
+  const char* rec = rec_at(p, cidx, hv);
+  const __bf16* aih = reinterpret_cast<const __bf16*>(rec);
+  const __bf16* ail = reinterpret_cast<const __bf16*>(rec + kMat);
+  const __bf16* aqp = reinterpret_cast<const __bf16*>(rec + 2 * kMat);
+  const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int off = (wid * 16 + l15) * kC + kk * 32 + 8 * lg;
+    ops.aiH[kk] = *reinterpret_cast<const bf8_t*>(aih + off);
+    ops.aiL[kk] = *reinterpret_cast<const bf8_t*>(ail + off);
+    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + off);
+  }
+  const int r4 = wid * 16 + 4 * lg;
+  ops.cq = *reinterpret_cast<const f4_t*>(sc + 0 * kC + r4);
+  ops.ed = *reinterpret_cast<const f4_t*>(sc + 3 * kC + r4);
+  ops.egl = sc[4 * kC];
+}
+
+// K rows of the lane's A operands written transposed: kt[k][token].
+template <int K>
+__device__ __forceinline__ void store_kt(__bf16 (*kt)[kLt], const bf8_t (&kA)[K / 32]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int row = wid * 16 + (lane & 15), lg = lane >> 4;
+#pragma unroll
+  for (int kk = 0; kk < K / 32; ++kk)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) kt[kk * 32 + 8 * lg + e][row] = kA[kk][e];
+}
+
+template <int K, typename T>
+// Two waves per SIMD (<= 256 registers per lane): two blocks share a CU.
+__global__ void __launch_bounds__(kTh) __attribute__((amdgpu_waves_per_eu(2)))
+gdn_chunk_state_kernel(ChunkParams p, int nvt) {
+  __shared__ P2Smem<K> sm;
+  constexpr int KK = K / 32;
+  const int tid = threadIdx.x;
+  const int wid = tid >> 6;
+  const int lane = tid & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  // XCD-aware mapping: the nvt V tiles of one (sequence, head) get block ids
+  // that are equal modulo 8, i.e. run on the same XCD and share its L2.
+  const int64_t w = blockIdx.x;
+  const int64_t xcd = w & 7, r = w >> 3;
+  const int vt = static_cast<int>(r % nvt);
+  const int64_t item = (r / nvt) * 8 + xcd;  // (sequence, head) index
+  if (item >= p.N * p.HV) return;            // whole block
+  const int64_t n = item / p.HV;
+  const int hv = static_cast<int>(item % p.HV);
+  const int hq = hv / (p.HV / p.H);
+  const int V = nvt * kBV;
+  const int v0 = vt * kBV;
+  const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
+  const int64_t cidx0 = p.chunk_off[n];
+  // Chunks of this sequence; the NTmax bound keeps a malformed cu_seqlens
+  // (never a well-formed one) from reading past the workspace.
+  const int64_t nch = max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.NTmax - cidx0));
+
+  // State rows (k) wid*(K/4) + m2*16 + 4*lg + i, columns nj*16 + l15.
+  constexpr int M2 = K / 64;
+  f4_t sreg[M2][2];
+#pragma unroll
+  for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
+        sreg[m2][nj][i] = p.h0 ? p.h0[((n * p.HV + hv) * K + kr) * V + v0 + nj * 16 + l15] : 0.f;
+      }
+  // bf16 hi / lo copy of the state for the K S operand.
+  auto publish_state = [&]() {
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj) {
+        Vec<__bf16, 4> h, l;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) split(sreg[m2][nj][i], h.v[i], l.v[i]);
+        const int k0 = wid * (K / 4) + m2 * 16 + 4 * lg;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][nj * 16 + l15][k0]) = h;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[1][nj * 16 + l15][k0]) = l;
+      }
+  };
+  publish_state();
+  const uint32_t vrow = static_cast<uint32_t>(p.HV) * V;  // v / o token stride
+  const int vcol0 = hv * V + v0;
+  EarlyOps<KK> opsA, opsB;
+  LateOps<KK> late;
+  if (nch > 0) {
+    const int L0 = static_cast<int>(min<int64_t>(kC, eos - bos));
+    load_early<K>(p, opsA, bos, L0, cidx0, hv, hq, vrow, vcol0);
+    load_late<K>(p, late, bos, L0, cidx0, hv, hq);
+    store_kt<K>(sm.kt[0], opsA.kA);
+  }
+  __syncthreads();
+
+  // One chunk: `cur` holds its early operands, `nxt` receives the next
+  // chunk's; `late` is reloaded for the next chunk at the end.
+  // The last chunk "prefetches" itself again (unused), so that every memory
+  // operation of the loop is unconditional.
+  auto step = [&](const EarlyOps<KK>& cur, EarlyOps<KK>& nxt, int64_t ci) {
+    const int64_t s = bos + ci * kC;
+    const int L = static_cast<int>(min<int64_t>(kC, eos - s));
+    const int64_t cn = min(ci + 1, nch - 1);
+    const int64_t sn = bos + cn * kC;
+    const int Ln = static_cast<int>(min<int64_t>(kC, eos - sn));
+    load_early<K>(p, nxt, sn, Ln, cidx0 + cn, hv, hq, vrow, vcol0);
+
+    // KS = K S (hi/lo S): rows wid*16.., columns nj*16..
+    f4_t ks[2];
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) ks[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj) {
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+        ks[nj] = mfma16(cur.kA[kk], sh, ks[nj]);
+        ks[nj] = mfma16(cur.kA[kk], sl, ks[nj]);
+      }
+    // R = b v - ck KS  ->  rt (transposed, hi / lo); padded rows are 0.
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      Vec<__bf16, 4> h, l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float rv = cur.bt[i] * to_f32(cur.v[nj][i]) - cur.ck[i] * ks[nj][i];
+        split(rv, h.v[i], l.v[i]);
+      }
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = h;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = l;
+    }
+    __syncthreads();  // (1) rt complete
+
+    // Vn = Ai R.
+    f4_t vn[2];
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      vn[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const bf8_t rh = *reinterpret_cast<const bf8_t*>(&sm.rt[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t rl = *reinterpret_cast<const bf8_t*>(&sm.rt[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+        vn[nj] = mfma_split3(late.aiH[kk], late.aiL[kk], rh, rl, vn[nj]);
+      }
+    }
+    // Vn -> vt (bf16), ed * Vn -> dt (hi / lo).
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      Vec<__bf16, 4> b, h, l;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        b.v[i] = static_cast<__bf16>(vn[nj][i]);
+        split(late.ed[i] * vn[nj][i], h.v[i], l.v[i]);
+      }
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.vt[nj * 16 + l15][wid * 16 + 4 * lg]) = b;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = h;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = l;
+    }
+    __syncthreads();  // (2) vt, dt complete; rt reads done
+
+    // o = cq (Q S) + Aq Vn, Q S with the hi part of S (sb is rewritten only
+    // after this).
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      f4_t qs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+        qs = mfma16(late.qA[kk], sh, qs);
+      }
+      f4_t acc;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[i] = late.cq[i] * qs[i];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        if (kk * 32 > wid * 16 + 15) continue;  // Aq columns beyond the diagonal
+        const bf8_t vb = *reinterpret_cast<const bf8_t*>(&sm.vt[nj * 16 + l15][kk * 32 + 8 * lg]);
+        acc = mfma16(late.aq[kk], vb, acc);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wid * 16 + 4 * lg + i;
+        T* dst = row < L ? reinterpret_cast<T*>(p.o) + static_cast<uint64_t>(s + row) * vrow +
+                               vcol0 + nj * 16 + l15
+                         : reinterpret_cast<T*>(p.dump) + row * kBV + nj * 16 + l15;
+        *dst = from_f32<T>(acc[i]);
+      }
+    }
+
+    // S <- exp(gc_last) S + K^T (ed Vn) on the wave's register rows, then
+    // its bf16 copy (every wave finished reading sb before barrier 1).
+    const __bf16 (*kt)[kLt] = sm.kt[ci & 1];
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2) {
+      const int mi = wid * M2 + m2;
+      bf8_t ka[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        ka[kk] = *reinterpret_cast<const bf8_t*>(&kt[mi * 16 + l15][kk * 32 + 8 * lg]);
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj) {
+        f4_t acc = sreg[m2][nj];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= late.egl;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const bf8_t dh = *reinterpret_cast<const bf8_t*>(&sm.dt[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+          const bf8_t dl = *reinterpret_cast<const bf8_t*>(&sm.dt[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+          acc = mfma16(ka[kk], dh, acc);
+          acc = mfma16(ka[kk], dl, acc);
+        }
+        sreg[m2][nj] = acc;
+      }
+    }
+    publish_state();
+    load_late<K>(p, late, sn, Ln, cidx0 + cn, hv, hq);  // this chunk is done with `late`
+    store_kt<K>(sm.kt[(ci + 1) & 1], nxt.kA);
+    __syncthreads();  // (3) state copy, next keys complete; vt / dt / kt reads done
+  };
+  // Unrolled by two so the operand buffers swap roles without copies.
+  for (int64_t ci = 0; ci < nch; ci += 2) {
+    step(opsA, opsB, ci);
+    if (ci + 1 < nch) step(opsB, opsA, ci + 1);
+  }
+  if (p.ht) {
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
+          p.ht[((n * p.HV + hv) * K + kr) * V + v0 + nj * 16 + l15] = sreg[m2][nj][i];
+        }
+  }
+}
+
+template <int K, typename GT, typename BT>
+int launch_chunk(const ChunkParams& p, int64_t V, hipStream_t s) {
+  hipLaunchKernelGGL(gdn_chunk_offsets_kernel, dim3(1), dim3(kTh), 0, s, p);
+  int st = launch_status();
+  if (st) return st;
+  hipLaunchKernelGGL((gdn_chunk_prep_kernel<K, GT, BT>), dim3(p.NTmax, (p.HV + 3) / 4),
+                     dim3(kTh), 0, s, p);
+  st = launch_status();
+  if (st) return st;
+  const int nvt = static_cast<int>(V / kBV);
+  const int64_t items = p.N * p.HV;
+  const int64_t blocks = cdiv(items, 8) * 8 * nvt;
+  hipLaunchKernelGGL((gdn_chunk_state_kernel<K, bf16>), dim3(blocks), dim3(kTh), 0, s, p, nvt);
+  return launch_status();
+}
+
+// g and beta each come in fp32 or bf16 (chunk.py's callers pass fp32 g and
+// bf16 beta).
+template <int K, typename GT>
+int chunk_beta(const ChunkParams& p, int64_t V, xk_dtype bdt, hipStream_t s) {
+  if (bdt == XK_F32) return launch_chunk<K, GT, float>(p, V, s);
+  if (bdt == XK_BF16) return launch_chunk<K, GT, bf16>(p, V, s);
+  return XK_ERR_UNSUPPORTED;
+}
+
+int64_t nt_max(int64_t total_tokens, int64_t N) { return total_tokens / kC + N; }
+
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t{255}; }
+
+}  // namespace
+}  // namespace xk
+
+using namespace xk;
+
+extern "C" int64_t xk_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t num_seqs,
+                                                int64_t HV) {
+  if (total_tokens < 0 || num_seqs < 0 || HV <= 0) return -1;
+  return align256(4 * (num_seqs + 1)) + kDump + nt_max(total_tokens, num_seqs) * HV * kRec;
+}
+
+extern "C" int xk_gdn_chunk_fwd(
+    const void* q, const void* k, const void* v, xk_dtype dtype, const void* g,
+    xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype, void* o,
+    const float* initial_state, float* final_state, const void* cu_seqlens,
+    xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
+    int64_t K, int64_t V, float scale, int use_qk_l2norm, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  if (N < 0 || total_tokens < 0 || H <= 0 || HV <= 0 || HV % H != 0)
+    return XK_ERR_INVALID;
+  // bf16 only, as the reference entry point (q/k feed the bf16 MFMA as-is).
+  if (dtype != XK_BF16) return XK_ERR_UNSUPPORTED;
+  if (g_dtype != XK_F32 && g_dtype != XK_BF16) return XK_ERR_UNSUPPORTED;
+  if (beta_dtype != XK_F32 && beta_dtype != XK_BF16) return XK_ERR_UNSUPPORTED;
+  if (cu_dtype != XK_I32 && cu_dtype != XK_I64) return XK_ERR_UNSUPPORTED;
+  if (K != 128 || V % kBV != 0 || V <= 0) return XK_ERR_UNSUPPORTED;
+  if (N == 0 || total_tokens == 0) return XK_OK;
+  if (!q || !k || !v || !g || !beta || !o || !cu_seqlens) return XK_ERR_INVALID;
+  if (!aligned(q, 16) || !aligned(k, 16)) return XK_ERR_INVALID;
+  const int64_t need = xk_gdn_chunk_workspace_bytes(total_tokens, N, HV);
+  if (!workspace || static_cast<int64_t>(workspace_bytes) < need) return XK_ERR_WORKSPACE;
+  if (!aligned(workspace, 256)) return XK_ERR_WORKSPACE;
+  ChunkParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = g;
+  p.beta = beta;
+  p.o = o;
+  p.h0 = initial_state;
+  p.ht = final_state;
+  p.cu = cu_seqlens;
+  p.cu_i64 = cu_dtype == XK_I64;
+  p.chunk_off = static_cast<int32_t*>(workspace);
+  p.dump = reinterpret_cast<bf16*>(static_cast<char*>(workspace) + align256(4 * (N + 1)));
+  p.rec = static_cast<char*>(workspace) + align256(4 * (N + 1)) + kDump;
+  p.N = N;
+  p.NTmax = nt_max(total_tokens, N);
+  p.T = total_tokens;
+  p.H = static_cast<int>(H);
+  p.HV = static_cast<int>(HV);
+  p.scale = scale;
+  p.l2norm = use_qk_l2norm;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (g_dtype == XK_F32) return chunk_beta<128, float>(p, V, beta_dtype, s);
+  return chunk_beta<128, bf16>(p, V, beta_dtype, s);
+}

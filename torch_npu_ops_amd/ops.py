@@ -391,6 +391,64 @@ def npu_fused_recurrent_gated_delta_rule(
     return o, final
 
 
+def npu_chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                               g: torch.Tensor, beta: torch.Tensor,
+                               scale: Optional[float] = None,
+                               initial_state: Optional[torch.Tensor] = None,
+                               output_final_state: bool = False,
+                               cu_seqlens: Optional[torch.Tensor] = None,
+                               head_first: bool = False,
+                               use_qk_l2norm_in_kernel: bool = False):
+    """Chunked gated delta rule (chunk 64); returns (o, final_state or None).
+
+    Mirrors npu_chunk_gated_delta_rule
+    (triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:556-642):
+    q, k [B, T, H, K], v [B, T, HV, V] bf16, g / beta [B, T, HV];
+    head_first must be False; initial_state [N, HV, K, V] (bf16 or fp32)
+    is read in fp32; the final state is fp32.  Without cu_seqlens the B
+    rows are B sequences of T tokens.  The whole pipeline runs on the
+    device with no host synchronisation.
+    """
+    if head_first:
+        raise ValueError("chunk_gated_delta_rule only supports head_first=false.")
+    if not (q.dtype == k.dtype == v.dtype == torch.bfloat16):
+        raise ValueError("chunk_gated_delta_rule expects q/k/v to be bfloat16.")
+    B, T, H, K = q.shape
+    HV, V = v.shape[2], v.shape[3]
+    if q.shape != k.shape:
+        raise ValueError("q and k must have the same shape.")
+    if HV % H:
+        raise ValueError("num_heads_v must be divisible by num_heads_qk")
+    if beta.shape != (B, T, HV) or g.shape != (B, T, HV):
+        raise ValueError("beta / g must have shape [B, T, H].")
+    dev = q.device
+    if cu_seqlens is None:
+        cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=dev)
+    else:
+        cu = cu_seqlens.contiguous()
+        if cu.dtype not in (torch.int32, torch.int64):
+            cu = cu.to(torch.int32)
+    N = cu.numel() - 1
+    total = B * T
+    sc = float(scale) if scale is not None else K ** -0.5
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    gc, bc = g.contiguous(), beta.contiguous()
+    h0 = None
+    if initial_state is not None:
+        h0 = initial_state.to(torch.float32).contiguous()
+    fin = torch.empty(N, HV, K, V, dtype=torch.float32, device=dev) if output_final_state else None
+    o = torch.empty(B, T, HV, V, dtype=q.dtype, device=dev)
+    ws_bytes = lib().xk_gdn_chunk_workspace_bytes(total, N, HV)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    st = lib().xk_gdn_chunk_fwd(
+        qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), xk_dtype(qc), gc.data_ptr(),
+        xk_dtype(gc), bc.data_ptr(), xk_dtype(bc), o.data_ptr(), _ptr(h0), _ptr(fin),
+        cu.data_ptr(), xk_dtype(cu), N, total, H, HV, K, V, sc,
+        int(use_qk_l2norm_in_kernel), ws.data_ptr(), ws.numel(), _stream(q))
+    check(st, "xk_gdn_chunk_fwd")
+    return o, fin
+
+
 def gdn_conv_decode(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
                     conv_weight: torch.Tensor, g: torch.Tensor,
                     beta: Optional[torch.Tensor], ssm_state: torch.Tensor,
