@@ -570,6 +570,22 @@ def time_cpu(case: Case):
     return statistics.median(ts) * scale, sample, len(ts)
 
 
+COPY_BYTES = 256 << 20
+
+
+def copy_calibration(dev, steps):
+    """Plain device copies of COPY_BYTES (read COPY_BYTES, write COPY_BYTES)
+    between buffers that rotate over 1 GiB, so that rocprofv3's FETCH_SIZE
+    and WRITE_SIZE per dispatch can be scaled to bytes."""
+    n = COPY_BYTES // 4
+    bufs = [torch.empty(n, dtype=torch.float32, device=dev).uniform_() for _ in range(5)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        bufs[(i + 1) % 5].copy_(bufs[i % 5])
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "dispatches": steps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -579,6 +595,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of a graph replay")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run plain 256 MiB device copies (the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
@@ -589,6 +608,9 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        copy_calibration(dev, args.steps)
+        return
     names = [args.op] if args.op else list(CASES)
     headline = args.op or HEADLINE
     ops = {}
@@ -646,6 +668,15 @@ def main():
                           f"config: {csec*1e3:.0f} ms/call"}
             print(f"[bench] cpu baseline {GdnChunkCase.name}: {csec*1e3:.0f} ms/call",
                   file=sys.stderr, flush=True)
+    # HBM bytes per dispatch of the headline kernel, as measured by the
+    # rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by a plain copy) that
+    # profiles/hbm_traffic_all_configs.md records; null if absent.
+    traffic = None
+    tpath = os.path.join(REPO, "profiles", "hbm_traffic_all_configs.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            t = json.load(f).get("traffic_bytes", {}).get(case.kernel)
+        traffic = round(t) if t is not None else None
     line = {
         "metric": "achieved HBM GB/s (% of peak) per op; chunked GDN prefill tokens/s",
         "value": head["GB/s"],
@@ -660,7 +691,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic: seeded torch.randn inputs of the BASELINE.json config",
         "config": {"workload": case.config, "op": headline},
-        "roofline": dict(head["roofline"], traffic=None),
+        "roofline": dict(head["roofline"], traffic=traffic),
         "cpu_baseline": cpu,
         "ops": ops,
     }

@@ -233,10 +233,11 @@ int xk_gdn_conv_decode(
  * output (a6b-a6g) in three launches with no host synchronisation.
  *   q, k : [total_tokens, H, K]; v, o : [total_tokens, HV, V] (dtype
  *   bf16, as the reference requires); g : [total_tokens, HV] log-decay,
- *   beta : [total_tokens, HV] (each fp32 or bf16); sequences cu_seqlens[n]..cu_seqlens[n+1] (int32 or
- *   int64, device).  initial_state / final_state : fp32 [N, HV, K, V] (NULL
- *   = zero / not written).  use_qk_l2norm applies x / sqrt(sum x^2 + 1e-6)
- *   to q and k first.  K = 128, V a multiple of 32.
+ *   beta : [total_tokens, HV] (each fp32 or bf16); sequences
+ *   cu_seqlens[n]..cu_seqlens[n+1] (int32 or int64, device).
+ *   initial_state / final_state : fp32 [N, HV, K, V] (NULL = zero / not
+ *   written).  use_qk_l2norm applies x / sqrt(sum x^2 + 1e-6) to q and k
+ *   first.  K = 128, V a multiple of 32.
  *   workspace >= xk_gdn_chunk_workspace_bytes(total_tokens, N, HV) bytes,
  *   256-byte aligned (chunk offsets + per-chunk inverse blocks).
  */
@@ -249,6 +250,83 @@ int xk_gdn_chunk_fwd(
     xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
     int64_t K, int64_t V, float scale, int use_qk_l2norm, void* workspace,
     size_t workspace_bytes, void* stream);
+
+/*
+ * a6b-a6g. The chunked pipeline stage by stage, in the reference's
+ * intermediate layouts (chunk size 64; chunks restart at every sequence):
+ *   g, g_cumsum, beta [T, H]; q, k [T, Hg, K]; v, u, v_new, o [T, H, V];
+ *   A, Ai [T, H, 64] (row t: row t - chunk start of the chunk's matrix);
+ *   w [T, H, K]; h [num_chunks, H, K, V] (chunks of all sequences in order).
+ * T = total_tokens; sequences by cu_seqlens (int32/int64, N + 1 entries,
+ * device).  K = 128 (V = 128 for w_u and fwd_o, a multiple of 32 for
+ * fwd_h); q/k/v/w/u/h bf16.  Decays are exp(x) for x <= 0, else 0.
+ * Except for the cumsum, every stage needs a workspace of
+ * xk_gdn_stage_workspace_bytes(N) bytes, 256-byte aligned.
+ */
+int64_t xk_gdn_stage_workspace_bytes(int64_t num_seqs);
+
+/* Per-chunk inclusive cumsum of g (fp32/bf16/f16) into fp32 out
+ * [T, H]; chunk_size a power of two.  Replaces npu_chunk_local_cumsum
+ * (triton_ops_api.h:34-37, npu_triton_chunk_gated_delta_rule.cpp:151-227);
+ * tokens outside every sequence get 0. */
+int xk_chunk_local_cumsum(const void* g, xk_dtype g_dtype, float* out,
+                          int64_t total_tokens, int64_t H,
+                          const void* cu_seqlens, xk_dtype cu_dtype, int64_t N,
+                          int64_t chunk_size, void* stream);
+
+/* A = strict_tril(beta_i (k_i . k_j) exp(gc_i - gc_j)), fp32 [T, H, 64];
+ * g_cumsum NULL = no decay.  Replaces npu_chunk_scaled_dot_kkt_fwd
+ * (triton_ops_api.h:39-44, npu_triton_chunk_gated_delta_rule.cpp:229-297). */
+int xk_chunk_scaled_dot_kkt(const void* k, xk_dtype dtype, const void* beta,
+                            xk_dtype beta_dtype, const float* g_cumsum,
+                            float* A, int64_t total_tokens, int64_t Hg,
+                            int64_t H, int64_t K, const void* cu_seqlens,
+                            xk_dtype cu_dtype, int64_t N, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* Ai = (I + A)^-1 per chunk (only the strictly lower part of A is read),
+ * written in ai_dtype (f32/bf16/f16).  Replaces npu_solve_tril
+ * (triton_ops_api.h:46-49, npu_triton_chunk_gated_delta_rule.cpp:299-395). */
+int xk_solve_tril(const float* A, void* Ai, xk_dtype ai_dtype,
+                  int64_t total_tokens, int64_t H, const void* cu_seqlens,
+                  xk_dtype cu_dtype, int64_t N, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* u = Ai (v beta), w = Ai (k beta exp(gc)); Ai bf16 or fp32, outputs bf16.
+ * Replaces npu_recompute_w_u_fwd (triton_ops_api.h:51-57,
+ * npu_triton_chunk_gated_delta_rule.cpp:397-475). */
+int xk_recompute_w_u(const void* k, const void* v, xk_dtype dtype,
+                     const void* beta, xk_dtype beta_dtype,
+                     const float* g_cumsum, const void* Ai, xk_dtype ai_dtype,
+                     void* w, void* u, int64_t total_tokens, int64_t Hg,
+                     int64_t H, int64_t K, int64_t V, const void* cu_seqlens,
+                     xk_dtype cu_dtype, int64_t N, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* The state recurrence: per chunk c, h[c] = state entering the chunk (bf16),
+ * v_new = u - w S (bf16, NULL = not stored), S <- exp(gc_last) S +
+ * k^T (v_new exp(gc_last - gc)); final_state fp32 [N, H, K, V] (NULL = not
+ * written); initial_state fp32 or NULL; g_cumsum NULL = no decay.  h holds
+ * num_chunks chunks.  Replaces npu_chunk_gated_delta_rule_fwd_h
+ * (triton_ops_api.h:124-135, npu_triton_chunk_gated_delta_rule.cpp:644-802). */
+int xk_chunk_fwd_h(const void* k, const void* w, const void* u, xk_dtype dtype,
+                   const float* g_cumsum, const float* initial_state, void* h,
+                   int64_t num_chunks, void* v_new, float* final_state,
+                   int64_t total_tokens, int64_t Hg, int64_t H, int64_t K,
+                   int64_t V, const void* cu_seqlens, xk_dtype cu_dtype,
+                   int64_t N, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* o = scale (exp(gc) (q h[c]) + tril(q k^T exp(gc_i - gc_j)) v), with the
+ * masked q k^T rounded to bf16 before the product as the reference does.
+ * Replaces npu_chunk_fwd_o (triton_ops_api.h:59-66,
+ * npu_triton_chunk_gated_delta_rule.cpp:477-554). */
+int xk_chunk_fwd_o(const void* q, const void* k, const void* v, const void* h,
+                   int64_t num_chunks, xk_dtype dtype, const float* g_cumsum,
+                   void* o, float scale, int64_t total_tokens, int64_t Hg,
+                   int64_t H, int64_t K, int64_t V, const void* cu_seqlens,
+                   xk_dtype cu_dtype, int64_t N, void* workspace,
+                   size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 } /* extern "C" */

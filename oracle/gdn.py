@@ -13,9 +13,15 @@ chunk_gdn: chunk_gated_delta_rule_full_op_ref of
   sequence, per head, per 64-token chunk: WY form with the row-recurrence
   inverse, then the state carry).
 
+Stage functions (kkt, solve_tril, recompute_w_u, chunk_fwd_h, chunk_fwd_o)
+restate the per-stage kernels of triton_npu/triton_src/chunk_gated_delta_rule
+(file:line in each docstring) on the reference's [T, H, ...] layouts.
+
 Pins (tests/test_oracle_gdn.py): beta = 0 and one-hot-key known answers,
 chunked == token-by-token recurrence in float64, the row-recurrence inverse
-== torch.linalg.solve_triangular, and per-chunk cumsum == torch.cumsum.
+== torch.linalg.solve_triangular, per-chunk cumsum == torch.cumsum, and the
+stage functions chained == chunk_gdn in float64 (so a mistake in any stage
+changes o or the final state).
 """
 from __future__ import annotations
 
@@ -158,3 +164,120 @@ def chunk_gdn(q, k, v, g, beta, scale: Optional[float], initial_state,
                  + (kc * torch.exp(gl[:, None] - gcc)[..., None]).transpose(1, 2) @ vn)
         fin[n, hi] = S
     return o.unsqueeze(0), fin
+
+
+# ---------------------------------------------------------------------------
+# Stage restatements.  Layouts: g, gc, beta [T, H]; q, k [T, Hg, K];
+# v, u, v_new, o [T, H, V]; A, Ai [T, H, 64]; w [T, H, K]; h [NT, H, K, V].
+# ---------------------------------------------------------------------------
+def _safe_exp(x):
+    """exp(x) for x <= 0, else 0 (utils.py:82-83)."""
+    return torch.where(x <= 0, torch.exp(torch.clamp(x, max=0)), torch.zeros_like(x))
+
+
+def _seq_chunks(cu, T, chunk=64):
+    """(sequence, first token, length) of every chunk, in order."""
+    out = []
+    for n, (a, b) in enumerate(_bounds(cu, 1, T)):
+        for s in range(a, b, chunk):
+            out.append((n, s, min(chunk, b - s)))
+    return out
+
+
+def chunk_scaled_dot_kkt(k, beta, gc, cu, dtype=torch.float32):
+    """A[t, h, j] = beta_t (k_t . k_{s+j}) exp(gc_t - gc_{s+j}) for j < t - s
+    (chunk_scaled_dot_kkt.py:20-86)."""
+    T, Hg, K = k.shape
+    H = beta.shape[1]
+    kf = k.to(dtype).repeat_interleave(H // Hg, 1)
+    A = torch.zeros(T, H, 64, dtype=dtype)
+    for _, s, L in _seq_chunks(cu, T):
+        kc = kf[s:s + L].transpose(0, 1)                      # [H, L, K]
+        a = kc @ kc.transpose(1, 2) * beta[s:s + L].to(dtype).t()[:, :, None]
+        if gc is not None:
+            g = gc[s:s + L].to(dtype).t()
+            a = a * _safe_exp(g[:, :, None] - g[:, None, :])
+        A[s:s + L, :, :L] = torch.tril(a, -1).transpose(0, 1)
+    return A
+
+
+def solve_tril(A, cu, dtype=torch.float32):
+    """Ai = (I + A)^-1 per chunk, by the row recurrence of
+    triton_chunk_gated_delta_rule_test.cpp:251-257 applied to -A
+    (solve_tril.py computes the same inverse blockwise)."""
+    T, H, _ = A.shape
+    Ai = torch.zeros(T, H, 64, dtype=dtype)
+    for _, s, L in _seq_chunks(cu, T):
+        M = -torch.tril(A[s:s + L, :, :L].to(dtype).transpose(0, 1), -1)  # [H, L, L]
+        for r in range(1, L):
+            M[:, r, :r] = M[:, r, :r] + (M[:, r:r + 1, :r] @ M[:, :r, :r])[:, 0]
+        M = M + torch.eye(L, dtype=dtype)
+        Ai[s:s + L, :, :L] = M.transpose(0, 1)
+    return Ai
+
+
+def recompute_w_u(k, v, beta, gc, Ai, cu, dtype=torch.float32):
+    """u = Ai (v beta), w = Ai (k beta exp(gc)) per chunk (wy_fast.py:21-87)."""
+    T, Hg, K = k.shape
+    H, V = v.shape[1], v.shape[2]
+    kf = k.to(dtype).repeat_interleave(H // Hg, 1)
+    w = torch.zeros(T, H, K, dtype=dtype)
+    u = torch.zeros(T, H, V, dtype=dtype)
+    for _, s, L in _seq_chunks(cu, T):
+        a = Ai[s:s + L, :, :L].to(dtype).transpose(0, 1)         # [H, L, L]
+        b = beta[s:s + L].to(dtype).t()[:, :, None]
+        eg = torch.exp(gc[s:s + L].to(dtype)).t()[:, :, None]
+        u[s:s + L] = (a @ (v[s:s + L].to(dtype).transpose(0, 1) * b)).transpose(0, 1)
+        w[s:s + L] = (a @ (kf[s:s + L].transpose(0, 1) * b * eg)).transpose(0, 1)
+    return w, u
+
+
+def chunk_fwd_h(k, w, u, gc, h0, cu, dtype=torch.float32):
+    """Per sequence and head, per chunk: h[c] = S (entering state),
+    v_new = u - w S, S <- exp(gc_last) S + k^T (v_new safe_exp(gc_last - gc))
+    (chunk_delta_h.py:22-198).  Returns (h [NT, H, K, V], v_new [T, H, V],
+    final [N, H, K, V])."""
+    T, Hg, K = k.shape
+    H, V = u.shape[1], u.shape[2]
+    kf = k.to(dtype).repeat_interleave(H // Hg, 1)
+    chunks = _seq_chunks(cu, T)
+    bounds = _bounds(cu, 1, T)
+    h = torch.zeros(len(chunks), H, K, V, dtype=dtype)
+    vnew = torch.zeros(T, H, V, dtype=dtype)
+    fin = torch.zeros(len(bounds), H, K, V, dtype=dtype)
+    S = {n: (h0[n].to(dtype).clone() if h0 is not None else torch.zeros(H, K, V, dtype=dtype))
+         for n in range(len(bounds))}
+    for c, (n, s, L) in enumerate(chunks):
+        h[c] = S[n]
+        vn = u[s:s + L].to(dtype).transpose(0, 1) - w[s:s + L].to(dtype).transpose(0, 1) @ S[n]
+        vnew[s:s + L] = vn.transpose(0, 1)
+        if gc is not None:
+            g = gc[s:s + L].to(dtype).t()                         # [H, L]
+            gl = g[:, L - 1]
+            vn = vn * _safe_exp(gl[:, None] - g)[:, :, None]
+            S[n] = S[n] * torch.exp(gl)[:, None, None]
+        S[n] = S[n] + kf[s:s + L].transpose(0, 1).transpose(1, 2) @ vn
+    for n in range(len(bounds)):
+        fin[n] = S[n]
+    return h, vnew, fin
+
+
+def chunk_fwd_o(q, k, v, h, gc, scale, cu, dtype=torch.float32):
+    """o = scale (exp(gc) (q h_c) + tril(q k^T safe_exp(gc_i - gc_j)) v) per
+    chunk (chunk_o.py:21-115)."""
+    T, Hg, K = q.shape
+    H, V = v.shape[1], v.shape[2]
+    qf = q.to(dtype).repeat_interleave(H // Hg, 1)
+    kf = k.to(dtype).repeat_interleave(H // Hg, 1)
+    o = torch.zeros(T, H, V, dtype=dtype)
+    for c, (_, s, L) in enumerate(_seq_chunks(cu, T)):
+        qc, kc = qf[s:s + L].transpose(0, 1), kf[s:s + L].transpose(0, 1)
+        vc = v[s:s + L].to(dtype).transpose(0, 1)
+        oc = qc @ h[c].to(dtype)
+        a = qc @ kc.transpose(1, 2)
+        if gc is not None:
+            g = gc[s:s + L].to(dtype).t()
+            oc = oc * torch.exp(g)[:, :, None]
+            a = a * _safe_exp(g[:, :, None] - g[:, None, :])
+        o[s:s + L] = (scale * (oc + torch.tril(a) @ vc)).transpose(0, 1)
+    return o

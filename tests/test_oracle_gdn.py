@@ -104,3 +104,48 @@ def test_spec_slots_follow_accepted_tokens():
     torch.testing.assert_close(o[:3], o0)
     torch.testing.assert_close(st[3], h0[0])
     assert torch.equal(st[0], pool[0]) and torch.equal(st[9], pool[9])
+
+
+def test_stages_chained_equal_whole_op():
+    """kkt -> solve_tril -> w/u -> fwd_h -> fwd_o (the reference's stage
+    kernels) must reproduce chunk_gdn (pinned against the recurrence above)
+    on varlen input with chunk-boundary and one-token sequences."""
+    g = torch.Generator().manual_seed(5)
+    cu = torch.tensor([0, 1, 65, 130, 200])
+    T, H, HV, K, V = 200, 2, 4, 16, 8
+    q = og.l2norm(_rand((1, T, H, K), g))
+    k = og.l2norm(_rand((1, T, H, K), g))
+    v = _rand((1, T, HV, V), g)
+    gate = -torch.rand(1, T, HV, generator=g, dtype=torch.float64)
+    beta = torch.sigmoid(_rand((1, T, HV), g))
+    h0 = _rand((4, HV, K, V), g)
+    scale = 0.37
+    ref_o, ref_s = og.chunk_gdn(q, k, v, gate, beta, scale, h0, cu, dtype=torch.float64)
+    f64 = torch.float64
+    gc = og.chunk_local_cumsum(gate, cu)[0]
+    A = og.chunk_scaled_dot_kkt(k[0], beta[0], gc, cu, dtype=f64)
+    Ai = og.solve_tril(A, cu, dtype=f64)
+    w, u = og.recompute_w_u(k[0], v[0], beta[0], gc, Ai, cu, dtype=f64)
+    h, vnew, fin = og.chunk_fwd_h(k[0], w, u, gc, h0, cu, dtype=f64)
+    o = og.chunk_fwd_o(q[0], k[0], vnew, h, gc, scale, cu, dtype=f64)
+    torch.testing.assert_close(o, ref_o[0], rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(fin, ref_s, rtol=1e-10, atol=1e-10)
+    # h[c] is the state entering chunk c: the first chunk of each sequence
+    # starts from h0, and 4 sequences of lengths 1, 64, 65, 70 give 1+1+2+2.
+    assert h.shape[0] == 6
+    for c, n in ((0, 0), (1, 1), (2, 2), (4, 3)):
+        torch.testing.assert_close(h[c], h0[n])
+
+
+def test_solve_tril_stage_matches_triangular_solve():
+    g = torch.Generator().manual_seed(6)
+    T, H = 100, 3
+    A = torch.tril(_rand((T, H, 64), g) * 0.3, -1)  # garbage above the diagonal is ignored
+    A = A + torch.triu(torch.ones(T, H, 64, dtype=torch.float64), 0) * 7.0
+    cu = torch.tensor([0, 40, 100])
+    Ai = og.solve_tril(A, cu, dtype=torch.float64)
+    for s, L in ((0, 40), (40, 60)):
+        for h in range(H):
+            m = torch.tril(A[s:s + L, h, :L], -1) + torch.eye(L, dtype=torch.float64)
+            ref = torch.linalg.solve_triangular(m, torch.eye(L, dtype=torch.float64), upper=False)
+            torch.testing.assert_close(Ai[s:s + L, h, :L], ref, rtol=1e-10, atol=1e-10)

@@ -61,6 +61,20 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "xk_gdn_chunk_fwd": (
         [P, P, P, INT, P, INT, P, INT, P, P, P, P, INT, I64, I64, I64, I64, I64,
          I64, F32, INT, P, SZ, P], INT),
+    "xk_gdn_stage_workspace_bytes": ([I64], I64),
+    "xk_chunk_local_cumsum": ([P, INT, P, I64, I64, P, INT, I64, I64, P], INT),
+    "xk_chunk_scaled_dot_kkt": (
+        [P, INT, P, INT, P, P, I64, I64, I64, I64, P, INT, I64, P, SZ, P], INT),
+    "xk_solve_tril": ([P, P, INT, I64, I64, P, INT, I64, P, SZ, P], INT),
+    "xk_recompute_w_u": (
+        [P, P, INT, P, INT, P, P, INT, P, P, I64, I64, I64, I64, I64, P, INT,
+         I64, P, SZ, P], INT),
+    "xk_chunk_fwd_h": (
+        [P, P, P, INT, P, P, P, I64, P, P, I64, I64, I64, I64, I64, P, INT, I64,
+         P, SZ, P], INT),
+    "xk_chunk_fwd_o": (
+        [P, P, P, P, I64, INT, P, P, F32, I64, I64, I64, I64, I64, P, INT, I64,
+         P, SZ, P], INT),
 }
 
 _LIB = None

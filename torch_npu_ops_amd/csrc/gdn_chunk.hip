@@ -39,12 +39,13 @@
 //    loaded into registers while chunk c computes, so the chain never waits
 //    on HBM.  Blocks of one (sequence, head) share an XCD (block id mod 8)
 //    and thus its L2 for the shared q/k/record reads.
-#include "xk_common.h"
+#include "gdn_common.h"
 
 namespace xk {
 namespace {
 
-constexpr int kC = 64;    // chunk size
+using namespace gdn;
+
 constexpr int kBV = 32;   // V columns per P2 block
 constexpr int kTh = 256;  // threads per block
 // Per-(chunk, head) record: ai_hi, ai_lo, aq (bf16 [64][64] each), then the
@@ -57,47 +58,6 @@ static_assert(kRec % 256 == 0, "records stay 256-byte aligned");
 // and stores in one in-order counter, and a store that only some paths
 // issue makes the compiler wait for every outstanding prefetch.
 constexpr int kDump = kC * kBV * 2;
-
-typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
-typedef float f4_t __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ f4_t mfma16(const bf8_t& a, const bf8_t& b, f4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// x = hi + lo with hi = bf16(x), lo = bf16(x - hi).
-__device__ __forceinline__ void split(float x, __bf16& hi, __bf16& lo) {
-  hi = static_cast<__bf16>(x);
-  lo = static_cast<__bf16>(x - static_cast<float>(hi));
-}
-
-// Eight consecutive fp32 values (16-byte aligned) split into hi / lo.
-__device__ __forceinline__ void split8(const float* p, bf8_t& h, bf8_t& l) {
-  const f4_t a = *reinterpret_cast<const f4_t*>(p);
-  const f4_t b = *reinterpret_cast<const f4_t*>(p + 4);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    __bf16 x, y;
-    split(a[e], x, y);
-    h[e] = x;
-    l[e] = y;
-    split(b[e], x, y);
-    h[e + 4] = x;
-    l[e + 4] = y;
-  }
-}
-
-__device__ __forceinline__ f4_t mfma_split3(const bf8_t& ah, const bf8_t& al, const bf8_t& bh,
-                                            const bf8_t& bl, f4_t c) {
-  c = mfma16(ah, bh, c);
-  c = mfma16(ah, bl, c);
-  return mfma16(al, bh, c);
-}
-
-template <typename T>
-__device__ __forceinline__ float ldf(const void* p, int64_t i) {
-  return to_f32(reinterpret_cast<const T*>(p)[i]);
-}
 
 struct ChunkParams {
   const void* q;  // [T, H, K]
@@ -120,86 +80,17 @@ struct ChunkParams {
   int l2norm;
 };
 
-// cu_seqlens[i], clamped to [0, T] so that a malformed table can never
-// index past the token rows (or the workspace sized from T).
-__device__ __forceinline__ int64_t cu_at(const ChunkParams& p, int64_t i) {
-  const int64_t v = p.cu_i64 ? reinterpret_cast<const int64_t*>(p.cu)[i]
-                             : static_cast<int64_t>(reinterpret_cast<const int32_t*>(p.cu)[i]);
-  return min(max(v, int64_t{0}), p.T);
-}
-
 __device__ __forceinline__ char* rec_at(const ChunkParams& p, int64_t c, int hv) {
   return p.rec + (c * p.HV + hv) * static_cast<int64_t>(kRec);
 }
 
-// P0: chunk_off[n] = sum_{m<n} ceil(len_m / 64).  One block.
-__global__ void __launch_bounds__(kTh) gdn_chunk_offsets_kernel(ChunkParams p) {
-  __shared__ int32_t part[kTh];
-  const int tid = threadIdx.x;
-  const int64_t per = (p.N + kTh - 1) / kTh;
-  const int64_t b0 = tid * per, b1 = min(p.N, b0 + per);
-  int32_t s = 0;
-  for (int64_t n = b0; n < b1; ++n) {
-    const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
-    s += static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
-  }
-  part[tid] = s;
-  __syncthreads();
-  if (tid == 0) {
-    int32_t acc = 0;
-    for (int i = 0; i < kTh; ++i) {
-      const int32_t v = part[i];
-      part[i] = acc;
-      acc += v;
-    }
-  }
-  __syncthreads();
-  int32_t acc = part[tid];
-  for (int64_t n = b0; n < b1; ++n) {
-    p.chunk_off[n] = acc;
-    const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
-    acc += static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
-  }
-  if (tid == kTh - 1) p.chunk_off[p.N] = acc;
-}
-
-// Locates global chunk c: sequence n, token start s, length L (<= 64).
-// Returns false if c is past the last chunk.
-__device__ __forceinline__ bool locate_chunk(const ChunkParams& p, int64_t c, int64_t& n,
-                                             int64_t& s, int& L) {
-  if (c >= p.chunk_off[p.N]) return false;
-  int64_t lo = 0, hi = p.N;  // chunk_off[lo] <= c < chunk_off[hi]
-  while (hi - lo > 1) {
-    const int64_t mid = (lo + hi) >> 1;
-    if (p.chunk_off[mid] <= c) lo = mid; else hi = mid;
-  }
-  n = lo;
-  const int64_t ci = c - p.chunk_off[n];
-  const int64_t a = cu_at(p, n), b = cu_at(p, n + 1);
-  s = a + ci * kC;
-  L = static_cast<int>(min<int64_t>(kC, b - s));
-  return true;
-}
-
-// Lane's MFMA operand of a 16-row slab of a [64 tokens x K] matrix in global
-// memory (token t of the slab at element (row0 + t) * row_stride + col_off):
-// row = r0 + (lane & 15), 8 elements from kk*32 + 8*(lane>>4).  Rows >= L
-// repeat row L-1 of the same chunk (branch-free, so the load never stalls
-// the wave); every consumer zeroes those rows through factors that are 0
-// there (beta, ck, ed, the masks of M and Aq).
-__device__ __forceinline__ bf8_t load_rows_op(const void* base, int64_t col_off, int64_t row0,
-                                              int L, int64_t row_stride, int r0, int kk) {
-  const int lane = threadIdx.x & 63;
-  const int r = min(r0 + (lane & 15), L - 1);
-  const bf16* src = reinterpret_cast<const bf16*>(base) + (row0 + r) * row_stride + col_off +
-                    kk * 32 + 8 * (lane >> 4);
-  return *reinterpret_cast<const bf8_t*>(src);
-}
+// Rows >= L of the K / Q operands (load_rows_op) repeat row L-1; here every
+// consumer zeroes them through factors that are 0 there (beta, ck, ed, the
+// masks of M and Aq).
 
 // ---------------------------------------------------------------------------
 // P1: one wave per (chunk, v-head); waves of a block are independent.
 // ---------------------------------------------------------------------------
-constexpr int kLd = kC + 4;  // fp32 LDS row stride: rows stay 16-byte aligned
 
 template <int K, typename GT, typename BT>
 __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
@@ -282,88 +173,7 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
     }
   __builtin_amdgcn_wave_barrier();
 
-  // Diagonal blocks: lane (b, cc) forms column cc of X_bb = (I + M_bb)^-1,
-  //   x[i] = delta_{i,cc} - sum_{j<i} M_bb[i][j] x[j].
-  const int b = lane >> 5, cc = lane & 31, base = b * 32;
-  float x[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const float* mr = &X[base + i][base];
-    float a0 = (i == cc) ? 1.f : 0.f, a1 = 0.f;
-#pragma unroll
-    for (int j = 0; j + 1 < i; j += 2) {
-      a0 = fmaf(-mr[j], x[j], a0);
-      a1 = fmaf(-mr[j + 1], x[j + 1], a1);
-    }
-    if (i & 1) a0 = fmaf(-mr[i - 1], x[i - 1], a0);
-    x[i] = a0 + a1;
-  }
-  __builtin_amdgcn_wave_barrier();
-  // X_00 transposed into the (spent) M_00 block, X_11 row-major into M_11.
-  if (b == 0) {
-#pragma unroll
-    for (int i = 0; i < 32; i += 4)
-      *reinterpret_cast<f4_t*>(&X[cc][i]) = f4_t{x[i], x[i + 1], x[i + 2], x[i + 3]};
-  } else {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) X[32 + i][32 + cc] = x[i];
-  }
-  __builtin_amdgcn_wave_barrier();
-
-  // T = M_10 X_00 (32 x 32), hi/lo-split operands.
-  f4_t tt[2][2];
-  {
-    bf8_t bh[2], bl[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) split8(&X[nt * 16 + l15][8 * lg], bh[nt], bl[nt]);
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      bf8_t ah, al;
-      split8(&X[32 + mt * 16 + l15][8 * lg], ah, al);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-        tt[mt][nt] = mfma_split3(ah, al, bh[nt], bl[nt], f4_t{0.f, 0.f, 0.f, 0.f});
-    }
-  }
-  // T transposed into the unused upper-right block: X[n][32 + k] = T[k][n].
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-      *reinterpret_cast<f4_t*>(&X[nt * 16 + l15][32 + mt * 16 + 4 * lg]) = tt[mt][nt];
-  __builtin_amdgcn_wave_barrier();
-  // X_10 = -X_11 T.
-  f4_t x10[2][2];
-  {
-    bf8_t bh[2], bl[2];
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt) split8(&X[nt * 16 + l15][32 + 8 * lg], bh[nt], bl[nt]);
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      bf8_t ah, al;
-      split8(&X[32 + mt * 16 + l15][32 + 8 * lg], ah, al);
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-        x10[mt][nt] = mfma_split3(ah, al, bh[nt], bl[nt], f4_t{0.f, 0.f, 0.f, 0.f});
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  // Assemble X = (I + M)^-1 row-major: X_10 over M_10, X_00 row-major over
-  // its transpose, zeros over T.
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) X[32 + mt * 16 + 4 * lg + i][nt * 16 + l15] = -x10[mt][nt][i];
-  if (b == 0) {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      X[i][cc] = x[i];
-      X[i][32 + cc] = 0.f;
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
+  invert_unit_lower(X);  // X = (I + M)^-1, row-major
 
   char* rec = rec_at(p, c, hv);
   __bf16* aih = reinterpret_cast<__bf16*>(rec);
@@ -758,7 +568,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 
 template <int K, typename GT, typename BT>
 int launch_chunk(const ChunkParams& p, int64_t V, hipStream_t s) {
-  hipLaunchKernelGGL(gdn_chunk_offsets_kernel, dim3(1), dim3(kTh), 0, s, p);
+  hipLaunchKernelGGL(chunk_offsets_kernel<ChunkParams>, dim3(1), dim3(256), 0, s, p);
   int st = launch_status();
   if (st) return st;
   hipLaunchKernelGGL((gdn_chunk_prep_kernel<K, GT, BT>), dim3(p.NTmax, (p.HV + 3) / 4),
@@ -782,8 +592,6 @@ int chunk_beta(const ChunkParams& p, int64_t V, xk_dtype bdt, hipStream_t s) {
 }
 
 int64_t nt_max(int64_t total_tokens, int64_t N) { return total_tokens / kC + N; }
-
-int64_t align256(int64_t x) { return (x + 255) & ~int64_t{255}; }
 
 }  // namespace
 }  // namespace xk

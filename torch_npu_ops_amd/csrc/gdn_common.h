@@ -1,0 +1,244 @@
+// Device building blocks shared by the chunked gated-delta-rule kernels
+// (the fused prefill in gdn_chunk.hip and the per-stage kernels in
+// gdn_stages.hip): 64-token chunk enumeration from cu_seqlens, bf16 MFMA
+// helpers with hi/lo-split fp32 operands, and the blocked inverse of a
+// 64x64 unit-lower-triangular matrix.
+#pragma once
+
+#include "xk_common.h"
+
+namespace xk {
+namespace gdn {
+
+constexpr int kC = 64;       // chunk size
+constexpr int kLd = kC + 4;  // fp32 LDS row stride: rows stay 16-byte aligned
+
+typedef __bf16 bf8_t __attribute__((ext_vector_type(8)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+// 16x16x32 bf16 MFMA.  Lane l holds A[l%16][8(l/16)+e], B[8(l/16)+e][l%16]
+// and C[4(l/16)+i][l%16].
+__device__ __forceinline__ f4_t mfma16(const bf8_t& a, const bf8_t& b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// x = hi + lo with hi = bf16(x), lo = bf16(x - hi): together ~16 mantissa
+// bits, so hi/lo-split products on the bf16 matrix cores stay within
+// ~2^-16 of fp32.
+__device__ __forceinline__ void split(float x, __bf16& hi, __bf16& lo) {
+  hi = static_cast<__bf16>(x);
+  lo = static_cast<__bf16>(x - static_cast<float>(hi));
+}
+
+// Eight consecutive fp32 values (16-byte aligned) split into hi / lo.
+__device__ __forceinline__ void split8(const float* p, bf8_t& h, bf8_t& l) {
+  const f4_t a = *reinterpret_cast<const f4_t*>(p);
+  const f4_t b = *reinterpret_cast<const f4_t*>(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    __bf16 x, y;
+    split(a[e], x, y);
+    h[e] = x;
+    l[e] = y;
+    split(b[e], x, y);
+    h[e + 4] = x;
+    l[e + 4] = y;
+  }
+}
+
+// (ah + al)(bh + bl) without the lo*lo term.
+__device__ __forceinline__ f4_t mfma_split3(const bf8_t& ah, const bf8_t& al, const bf8_t& bh,
+                                            const bf8_t& bl, f4_t c) {
+  c = mfma16(ah, bh, c);
+  c = mfma16(ah, bl, c);
+  return mfma16(al, bh, c);
+}
+
+template <typename T>
+__device__ __forceinline__ float ldf(const void* p, int64_t i) {
+  return to_f32(reinterpret_cast<const T*>(p)[i]);
+}
+
+// exp(x) for x <= 0, else 0 (the masked decay of the chunk kernels,
+// triton_npu/triton_src/chunk_gated_delta_rule/utils.py:82-83).
+__device__ __forceinline__ float safe_exp(float x) { return x <= 0.f ? __expf(x) : 0.f; }
+
+// ---------------------------------------------------------------------------
+// Sequences and chunks.  P provides cu (int32 or int64 [N+1], cu_i64), N,
+// T (token rows) and chunk_off (int32 [N+1] device workspace).
+// ---------------------------------------------------------------------------
+
+// cu_seqlens[i], clamped to [0, T] so that a malformed table can never index
+// past the token rows (or a workspace sized from T).
+template <class P>
+__device__ __forceinline__ int64_t cu_at(const P& p, int64_t i) {
+  const int64_t v = p.cu_i64 ? reinterpret_cast<const int64_t*>(p.cu)[i]
+                             : static_cast<int64_t>(reinterpret_cast<const int32_t*>(p.cu)[i]);
+  return min(max(v, int64_t{0}), p.T);
+}
+
+// chunk_off[n] = sum_{m<n} ceil(len_m / 64), chunk_off[N] = total chunks.
+// One block of 256 threads.
+template <class P>
+__global__ void __launch_bounds__(256) chunk_offsets_kernel(P p) {
+  constexpr int kT = 256;
+  __shared__ int32_t part[kT];
+  const int tid = threadIdx.x;
+  const int64_t per = (p.N + kT - 1) / kT;
+  const int64_t b0 = tid * per, b1 = min(p.N, b0 + per);
+  int32_t s = 0;
+  for (int64_t n = b0; n < b1; ++n) {
+    const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
+    s += static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+  }
+  part[tid] = s;
+  __syncthreads();
+  if (tid == 0) {
+    int32_t acc = 0;
+    for (int i = 0; i < kT; ++i) {
+      const int32_t v = part[i];
+      part[i] = acc;
+      acc += v;
+    }
+  }
+  __syncthreads();
+  int32_t acc = part[tid];
+  for (int64_t n = b0; n < b1; ++n) {
+    p.chunk_off[n] = acc;
+    const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
+    acc += static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+  }
+  if (tid == kT - 1) p.chunk_off[p.N] = acc;
+}
+
+// Global chunk c -> sequence n, first token s, length L (1..64); false if c
+// is past the last chunk.
+template <class P>
+__device__ __forceinline__ bool locate_chunk(const P& p, int64_t c, int64_t& n, int64_t& s,
+                                             int& L) {
+  if (c >= p.chunk_off[p.N]) return false;
+  int64_t lo = 0, hi = p.N;  // chunk_off[lo] <= c < chunk_off[hi]
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (p.chunk_off[mid] <= c) lo = mid; else hi = mid;
+  }
+  n = lo;
+  const int64_t ci = c - p.chunk_off[n];
+  const int64_t a = cu_at(p, n), b = cu_at(p, n + 1);
+  s = a + ci * kC;
+  L = static_cast<int>(min<int64_t>(kC, b - s));
+  return true;
+}
+
+// Lane's MFMA operand of a 16-row slab of a [64 tokens x K] bf16 matrix in
+// global memory (token t of the slab at element (row0 + t) * row_stride +
+// col_off): row = r0 + (lane & 15), 8 elements from kk*32 + 8*(lane>>4).
+// Rows >= L repeat row L-1 of the same chunk (branch-free, so the load never
+// stalls the wave); every consumer zeroes or drops those rows.
+__device__ __forceinline__ bf8_t load_rows_op(const void* base, int64_t col_off, int64_t row0,
+                                              int L, int64_t row_stride, int r0, int kk) {
+  const int lane = threadIdx.x & 63;
+  const int r = min(r0 + (lane & 15), L - 1);
+  const bf16* src = reinterpret_cast<const bf16*>(base) + (row0 + r) * row_stride + col_off +
+                    kk * 32 + 8 * (lane >> 4);
+  return *reinterpret_cast<const bf8_t*>(src);
+}
+
+// ---------------------------------------------------------------------------
+// X <- (I + M)^-1 for a strictly lower M in the wave's LDS tile X (only the
+// strictly lower entries of the ten lower 16x16 tiles are read); the result
+// is written back row-major (fp32, zeros above the diagonal).  One wave.
+//   * the two 32x32 diagonal blocks by forward substitution, lane (b, cc)
+//     forming column cc of X_bb: x[i] = delta_{i,cc} - sum_{j<i} M[i][j] x[j];
+//   * the off-diagonal block X_10 = -X_11 (M_10 X_00) with hi/lo-split MFMAs.
+// This is the 16->64 block merge of solve_tril.py:266-320 with 32-wide
+// diagonal blocks.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void invert_unit_lower(float (*X)[kLd]) {
+  const int lane = threadIdx.x & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  const int b = lane >> 5, cc = lane & 31, base = b * 32;
+  float x[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float* mr = &X[base + i][base];
+    float a0 = (i == cc) ? 1.f : 0.f, a1 = 0.f;
+#pragma unroll
+    for (int j = 0; j + 1 < i; j += 2) {
+      a0 = fmaf(-mr[j], x[j], a0);
+      a1 = fmaf(-mr[j + 1], x[j + 1], a1);
+    }
+    if (i & 1) a0 = fmaf(-mr[i - 1], x[i - 1], a0);
+    x[i] = a0 + a1;
+  }
+  __builtin_amdgcn_wave_barrier();
+  // X_00 transposed into the (spent) M_00 block, X_11 row-major into M_11.
+  if (b == 0) {
+#pragma unroll
+    for (int i = 0; i < 32; i += 4)
+      *reinterpret_cast<f4_t*>(&X[cc][i]) = f4_t{x[i], x[i + 1], x[i + 2], x[i + 3]};
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) X[32 + i][32 + cc] = x[i];
+  }
+  __builtin_amdgcn_wave_barrier();
+
+  // T = M_10 X_00 (32 x 32).
+  f4_t tt[2][2];
+  {
+    bf8_t bh[2], bl[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) split8(&X[nt * 16 + l15][8 * lg], bh[nt], bl[nt]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      bf8_t ah, al;
+      split8(&X[32 + mt * 16 + l15][8 * lg], ah, al);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        tt[mt][nt] = mfma_split3(ah, al, bh[nt], bl[nt], f4_t{0.f, 0.f, 0.f, 0.f});
+    }
+  }
+  // T transposed into the unused upper-right block: X[n][32 + k] = T[k][n].
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+      *reinterpret_cast<f4_t*>(&X[nt * 16 + l15][32 + mt * 16 + 4 * lg]) = tt[mt][nt];
+  __builtin_amdgcn_wave_barrier();
+  // X_10 = -X_11 T.
+  f4_t x10[2][2];
+  {
+    bf8_t bh[2], bl[2];
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) split8(&X[nt * 16 + l15][32 + 8 * lg], bh[nt], bl[nt]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      bf8_t ah, al;
+      split8(&X[32 + mt * 16 + l15][32 + 8 * lg], ah, al);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        x10[mt][nt] = mfma_split3(ah, al, bh[nt], bl[nt], f4_t{0.f, 0.f, 0.f, 0.f});
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  // Assemble row-major: X_10 over M_10, X_00 over its transpose, zeros over T.
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) X[32 + mt * 16 + 4 * lg + i][nt * 16 + l15] = -x10[mt][nt][i];
+  if (b == 0) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      X[i][cc] = x[i];
+      X[i][32 + cc] = 0.f;
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+}
+
+inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t{255}; }
+
+}  // namespace gdn
+}  // namespace xk

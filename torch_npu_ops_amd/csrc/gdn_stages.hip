@@ -1,0 +1,764 @@
+// The chunked gated delta rule as separate stages (a6b..a6g), each with the
+// tensor layout of the reference stage it replaces, for callers that drive
+// the pipeline stage by stage (triton_npu/torch_api/triton_ops_api.h:34-66,
+// 124-135).  The fused xk_gdn_chunk_fwd computes the same result in three
+// launches without these intermediates.
+//
+// Layouts (rows = tokens of all sequences, cu_seqlens gives the sequences;
+// chunks of 64 tokens restart at every sequence start):
+//   g, g_cumsum, beta  [T, H]          k, q  [T, Hg, K]     v, u, v_new, o [T, H, V]
+//   A, Ai              [T, H, 64]      w     [T, H, K]      h [NT, H, K, V]
+// where row t of A / Ai holds row (t - chunk start) of that chunk's 64x64
+// matrix and NT counts the chunks of all sequences in order.
+//
+// Stage semantics (fp32 arithmetic; decays are exp(x) for x <= 0, else 0):
+//   cumsum   g_cumsum = per-chunk inclusive cumsum of g           (cumsum.py)
+//   kkt      A[i][j] = b_i (k_i . k_j) exp(gc_i - gc_j), i > j     (chunk_scaled_dot_kkt.py:20-86)
+//   solve    Ai = (I + A)^-1                                       (solve_tril.py)
+//   w_u      u = Ai (v b),  w = Ai (k b exp(gc))                   (wy_fast.py:21-87)
+//   fwd_h    per chunk: h_c = S;  v_new = u - w S;
+//            S <- exp(gc_last) S + k^T (v_new exp(gc_last - gc))    (chunk_delta_h.py:22-198)
+//   fwd_o    o = scale (exp(gc) (q h_c) + tril(q k^T exp(gc_i - gc_j)) v_new)
+//                                                                  (chunk_o.py:21-115)
+#include "gdn_common.h"
+
+namespace xk {
+namespace {
+
+using namespace gdn;
+
+constexpr int kTh = 256;
+
+// Common sequence fields (read by cu_at / locate_chunk / chunk_offsets_kernel).
+struct Seq {
+  const void* cu;
+  int cu_i64;
+  int64_t N;
+  int64_t T;  // token rows
+  int32_t* chunk_off;
+  int64_t NTmax;
+};
+
+// ---------------------------------------------------------------------------
+// a6b: per-chunk cumsum.  One thread per (token, head).
+// ---------------------------------------------------------------------------
+struct CumsumParams : Seq {
+  const void* g;
+  float* out;
+  int H;
+  int chunk;
+};
+
+template <typename GT>
+__global__ void __launch_bounds__(kTh) chunk_cumsum_kernel(CumsumParams p) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kTh + threadIdx.x;
+  if (idx >= p.T * p.H) return;
+  const int64_t t = idx / p.H;
+  const int h = static_cast<int>(idx - t * p.H);
+  float acc = 0.f;
+  if (t >= cu_at(p, 0) && t < cu_at(p, p.N)) {
+    int64_t lo = 0, hi = p.N;  // cu[lo] <= t < cu[hi]
+    while (hi - lo > 1) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (cu_at(p, mid) <= t) lo = mid; else hi = mid;
+    }
+    const int64_t bos = cu_at(p, lo);
+    const int64_t cs = bos + ((t - bos) / p.chunk) * p.chunk;
+    for (int64_t j = cs; j <= t; ++j) acc += ldf<GT>(p.g, j * p.H + h);
+  }
+  p.out[idx] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// a6c: A = strict_tril(b_i (k_i . k_j) exp(gc_i - gc_j)).  One wave per
+// (chunk, head); the four waves of a block take four heads.
+// ---------------------------------------------------------------------------
+struct KktParams : Seq {
+  const void* k;
+  const void* beta;
+  const float* gcum;  // or NULL
+  float* A;
+  int H, Hg;
+};
+
+template <int K, typename BT>
+__global__ void __launch_bounds__(kTh) chunk_kkt_kernel(KktParams p) {
+  __shared__ float vec[4][2][kC];  // gc, beta per wave
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  const int h = blockIdx.y * 4 + wid;
+  int64_t n, s;
+  int L;
+  if (!(h < p.H && locate_chunk(p, blockIdx.x, n, s, L))) return;  // wave-uniform
+  const int hq = h / (p.H / p.Hg);
+  constexpr int KK = K / 32;
+  bf8_t kop[4][KK];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      kop[mi][kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L,
+                                 static_cast<int64_t>(p.Hg) * K, mi * 16, kk);
+  const int lt = min(lane, L - 1);
+  vec[wid][0][lane] = p.gcum ? p.gcum[(s + lt) * p.H + h] : 0.f;
+  vec[wid][1][lane] = ldf<BT>(p.beta, (s + lt) * p.H + h);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 4; ++nj) {
+      f4_t a = {0.f, 0.f, 0.f, 0.f};
+      if (nj <= mi) {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) a = mfma16(kop[mi][kk], kop[nj][kk], a);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = mi * 16 + 4 * lg + i, col = nj * 16 + l15;
+        if (row < L) {
+          float val = 0.f;
+          if (row > col) {
+            val = vec[wid][1][row] * a[i];
+            if (p.gcum) val *= safe_exp(vec[wid][0][row] - vec[wid][0][col]);
+          }
+          p.A[((s + row) * p.H + h) * kC + col] = val;
+        }
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// a6d: Ai = (I + A)^-1 per chunk.  One wave per (chunk, head).
+// ---------------------------------------------------------------------------
+struct TrilParams : Seq {
+  const float* A;
+  void* Ai;
+  int H;
+};
+
+template <typename OT>
+__global__ void __launch_bounds__(kTh) solve_tril_kernel(TrilParams p) {
+  __shared__ __align__(16) float lds[4][kC][kLd];
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int h = blockIdx.y * 4 + wid;
+  int64_t n, s;
+  int L;
+  if (!(h < p.H && locate_chunk(p, blockIdx.x, n, s, L))) return;  // wave-uniform
+  float (*X)[kLd] = lds[wid];
+  // Lane r loads row r (strictly lower part; rows >= L are zero).
+  const float* src = p.A + ((s + min(lane, L - 1)) * p.H + h) * kC;
+#pragma unroll
+  for (int j0 = 0; j0 < kC; j0 += 4) {
+    const f4_t a = *reinterpret_cast<const f4_t*>(src + j0);
+    f4_t m;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) m[e] = (lane < L && j0 + e < lane) ? a[e] : 0.f;
+    *reinterpret_cast<f4_t*>(&X[lane][j0]) = m;
+  }
+  __builtin_amdgcn_wave_barrier();
+  invert_unit_lower(X);
+  if (lane < L) {
+    OT* dst = reinterpret_cast<OT*>(p.Ai) + ((s + lane) * p.H + h) * kC;
+#pragma unroll
+    for (int j = 0; j < kC; ++j) dst[j] = from_f32<OT>(X[lane][j]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a6e: u = Ai (v b), w = Ai (k b exp(gc)).  One block per (chunk, head); the
+// right-hand side is staged transposed (token-contiguous) as bf16 hi / lo,
+// wave w produces output columns [w*D/4, (w+1)*D/4) of all 64 rows.
+// ---------------------------------------------------------------------------
+struct WuParams : Seq {
+  const void* k;
+  const void* v;
+  const void* beta;
+  const float* gcum;
+  const void* Ai;
+  void* w;
+  void* u;
+  int H, Hg;
+};
+
+constexpr int kLt = kC + 8;  // bf16 LDS row stride (144 B: 16-byte aligned)
+
+template <int D, typename AT>
+__device__ __forceinline__ void wu_product(const WuParams& p, __bf16 (*bt)[D][kLt], int64_t s,
+                                           int L, int h, void* out) {
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  constexpr int NJ = D / 64;  // 16-column tiles per wave
+  f4_t acc[4][NJ];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    const AT* arow = reinterpret_cast<const AT*>(p.Ai) +
+                     ((s + min(mi * 16 + l15, L - 1)) * p.H + h) * kC + 8 * lg;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf8_t ah, al;
+      if constexpr (std::is_same<AT, float>::value) {
+        split8(arow + kk * 32, ah, al);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          ah[e] = static_cast<__bf16>(to_f32(arow[kk * 32 + e]));
+          al[e] = static_cast<__bf16>(0.f);
+        }
+      }
+#pragma unroll
+      for (int nj = 0; nj < NJ; ++nj) {
+        const int col = wid * (D / 4) + nj * 16 + l15;
+        const bf8_t bh = *reinterpret_cast<const bf8_t*>(&bt[0][col][kk * 32 + 8 * lg]);
+        const bf8_t bl = *reinterpret_cast<const bf8_t*>(&bt[1][col][kk * 32 + 8 * lg]);
+        acc[mi][nj] = mfma16(ah, bh, acc[mi][nj]);
+        acc[mi][nj] = mfma16(ah, bl, acc[mi][nj]);
+        if constexpr (std::is_same<AT, float>::value) acc[mi][nj] = mfma16(al, bh, acc[mi][nj]);
+      }
+    }
+  }
+  bf16* o = reinterpret_cast<bf16*>(out);
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < NJ; ++nj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = mi * 16 + 4 * lg + i;
+        if (row < L)
+          o[((s + row) * p.H + h) * D + wid * (D / 4) + nj * 16 + l15] = from_f32<bf16>(acc[mi][nj][i]);
+      }
+}
+
+// Rows t < L of src (row stride `rs`, bf16) times f[t] into bt (transposed,
+// hi / lo); rows >= L are zero.
+template <int D>
+__device__ __forceinline__ void stage_scaled_t(__bf16 (*bt)[D][kLt], const bf16* src, int64_t rs,
+                                               const float* f, int L) {
+  for (int i = threadIdx.x; i < kC * (D / 8); i += kTh) {
+    const int t = i / (D / 8), c0 = (i % (D / 8)) * 8;
+    const Vec<bf16, 8> x = *reinterpret_cast<const Vec<bf16, 8>*>(src + min(t, L - 1) * rs + c0);
+    const float sc = t < L ? f[t] : 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 hi, lo;
+      split(sc * to_f32(x.v[e]), hi, lo);
+      bt[0][c0 + e][t] = hi;
+      bt[1][c0 + e][t] = lo;
+    }
+  }
+}
+
+template <typename BT, typename AT>
+__global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
+  constexpr int D = 128;  // K = V = 128
+  __shared__ __align__(16) __bf16 bt[2][D][kLt];
+  __shared__ float fb[kC], fk[kC];
+  const int h = blockIdx.y;
+  int64_t n, s;
+  int L;
+  if (!locate_chunk(p, blockIdx.x, n, s, L)) return;  // block-uniform
+  const int hq = h / (p.H / p.Hg);
+  if (threadIdx.x < kC) {
+    const int t = min(static_cast<int>(threadIdx.x), L - 1);
+    const float b = ldf<BT>(p.beta, (s + t) * p.H + h);
+    fb[threadIdx.x] = b;
+    fk[threadIdx.x] = b * __expf(p.gcum ? p.gcum[(s + t) * p.H + h] : 0.f);
+  }
+  __syncthreads();
+  stage_scaled_t<D>(bt, reinterpret_cast<const bf16*>(p.v) + (s * p.H + h) * D,
+                    static_cast<int64_t>(p.H) * D, fb, L);
+  __syncthreads();
+  wu_product<D, AT>(p, bt, s, L, h, p.u);
+  __syncthreads();
+  stage_scaled_t<D>(bt, reinterpret_cast<const bf16*>(p.k) + (s * p.Hg + hq) * D,
+                    static_cast<int64_t>(p.Hg) * D, fk, L);
+  __syncthreads();
+  wu_product<D, AT>(p, bt, s, L, h, p.w);
+}
+
+// ---------------------------------------------------------------------------
+// a6f: the state recurrence with per-chunk state snapshots.  One 256-lane
+// block per (sequence, head, 32-column V tile); the fp32 state lives in
+// registers (wave w: K rows [32w, 32w+32)), its bf16 hi / lo copy in LDS.
+// ---------------------------------------------------------------------------
+constexpr int kBV = 32;
+
+struct FwdHParams : Seq {
+  const void* k;
+  const void* w;
+  const void* u;
+  const float* gcum;  // or NULL
+  const float* h0;    // or NULL
+  void* h;            // [NT, H, K, V]
+  void* vnew;         // or NULL
+  float* ht;          // or NULL
+  int64_t hcap;       // chunks h holds
+  int H, Hg;
+  int nvt;
+};
+
+template <int K>
+struct __align__(16) FwdHSmem {
+  __bf16 sb[2][kBV][K + 8];  // state hi / lo, transposed: sb[h][v][k]
+  __bf16 kt[K][kLt];         // chunk keys transposed
+  __bf16 dt[2][kBV][kLt];    // decayed v_new transposed, hi / lo
+  float gc[kC];
+};
+
+template <int K>
+__global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
+  __shared__ FwdHSmem<K> sm;
+  constexpr int KK = K / 32, M2 = K / 64;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  const int64_t bid = blockIdx.x;
+  const int64_t r = bid >> 3;
+  const int vt = static_cast<int>(r % p.nvt);
+  const int64_t item = (r / p.nvt) * 8 + (bid & 7);  // same XCD for one (n, h)
+  if (item >= p.N * p.H) return;
+  const int64_t n = item / p.H;
+  const int h = static_cast<int>(item % p.H);
+  const int hq = h / (p.H / p.Hg);
+  const int V = p.nvt * kBV, v0 = vt * kBV;
+  const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
+  const int64_t c0 = p.chunk_off[n];
+  // Chunks of this sequence, bounded by the snapshots h can hold (never
+  // binding for a well-formed cu_seqlens).
+  const int64_t nch = max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.hcap - c0));
+  f4_t sreg[M2][2];
+#pragma unroll
+  for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
+        sreg[m2][nj][i] = p.h0 ? p.h0[((n * p.H + h) * K + kr) * V + v0 + nj * 16 + l15] : 0.f;
+      }
+  const int64_t krow = static_cast<int64_t>(p.Hg) * K;
+  for (int64_t ci = 0; ci < nch; ++ci) {
+    const int64_t s = bos + ci * kC;
+    const int L = static_cast<int>(min<int64_t>(kC, eos - s));
+    const int64_t cidx = c0 + ci;
+    // Snapshot of the state entering this chunk, and its bf16 hi / lo copy.
+    bf16* hdst = reinterpret_cast<bf16*>(p.h) + (cidx * p.H + h) * static_cast<int64_t>(K) * V;
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj) {
+        Vec<__bf16, 4> hi, lo;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
+          hdst[static_cast<int64_t>(kr) * V + v0 + nj * 16 + l15] = from_f32<bf16>(sreg[m2][nj][i]);
+          split(sreg[m2][nj][i], hi.v[i], lo.v[i]);
+        }
+        const int k0 = wid * (K / 4) + m2 * 16 + 4 * lg;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][nj * 16 + l15][k0]) = hi;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[1][nj * 16 + l15][k0]) = lo;
+      }
+    // Keys transposed; per-token gc.
+    bf8_t ka[KK];
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      ka[kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, krow, wid * 16, kk);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sm.kt[kk * 32 + 8 * lg + e][wid * 16 + l15] = ka[kk][e];
+    }
+    if (tid < kC) sm.gc[tid] = p.gcum ? p.gcum[(s + min(tid, L - 1)) * p.H + h] : 0.f;
+    __syncthreads();
+    // WS = w S (hi / lo S) for rows wid*16.., then v_new = u - WS.
+    f4_t ws[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const bf8_t wa = load_rows_op(p.w, static_cast<int64_t>(h) * K, s, L,
+                                    static_cast<int64_t>(p.H) * K, wid * 16, kk);
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj) {
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+        ws[nj] = mfma16(wa, sh, ws[nj]);
+        ws[nj] = mfma16(wa, sl, ws[nj]);
+      }
+    }
+    const float gl = sm.gc[L - 1];
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      Vec<__bf16, 4> dh, dl;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wid * 16 + 4 * lg + i;
+        const int rr = min(row, L - 1);
+        const int64_t off = ((s + rr) * p.H + h) * static_cast<int64_t>(V) + v0 + nj * 16 + l15;
+        const float vn = to_f32(reinterpret_cast<const bf16*>(p.u)[off]) - ws[nj][i];
+        if (p.vnew && row < L) reinterpret_cast<bf16*>(p.vnew)[off] = from_f32<bf16>(vn);
+        const float dec = row < L ? (p.gcum ? safe_exp(gl - sm.gc[row]) : 1.f) : 0.f;
+        split(vn * dec, dh.v[i], dl.v[i]);
+      }
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = dh;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = dl;
+    }
+    __syncthreads();
+    // S <- exp(gl) S + K^T D.
+    const float egl = p.gcum ? __expf(gl) : 1.f;
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2) {
+      const int mi = wid * M2 + m2;
+      bf8_t kA[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        kA[kk] = *reinterpret_cast<const bf8_t*>(&sm.kt[mi * 16 + l15][kk * 32 + 8 * lg]);
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj) {
+        f4_t acc = sreg[m2][nj];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= egl;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const bf8_t dh = *reinterpret_cast<const bf8_t*>(&sm.dt[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+          const bf8_t dl = *reinterpret_cast<const bf8_t*>(&sm.dt[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+          acc = mfma16(kA[kk], dh, acc);
+          acc = mfma16(kA[kk], dl, acc);
+        }
+        sreg[m2][nj] = acc;
+      }
+    }
+    __syncthreads();  // sb / kt / dt / gc are rewritten by the next chunk
+  }
+  if (p.ht) {
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
+          p.ht[((n * p.H + h) * K + kr) * V + v0 + nj * 16 + l15] = sreg[m2][nj][i];
+        }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// a6g: o = scale (exp(gc) (q h_c) + tril(q k^T exp(gc_i - gc_j)) v_new).
+// One block per (chunk, head): h_c and v_new staged transposed in LDS, wave
+// w owns rows [16w, 16w+16) and all V columns.
+// ---------------------------------------------------------------------------
+struct FwdOParams : Seq {
+  const void* q;
+  const void* k;
+  const void* v;
+  const void* h;
+  const float* gcum;  // or NULL
+  void* o;
+  float scale;
+  int64_t hcap;  // chunks h holds
+  int H, Hg;
+};
+
+template <int K, int V>
+struct __align__(16) FwdOSmem {
+  __bf16 ht[V][K + 8];   // h_c transposed: ht[v][k]
+  __bf16 vt[V][kLt];     // v_new transposed: vt[v][token]
+  __bf16 aq[kC][kLt];    // masked q k^T, row-major
+  float gc[kC];
+};
+
+template <int K, int V>
+__global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
+  __shared__ FwdOSmem<K, V> sm;
+  constexpr int KK = K / 32, NJ = V / 16;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  const int h = blockIdx.y;
+  const int64_t c = blockIdx.x;
+  int64_t n, s;
+  int L;
+  if (!locate_chunk(p, c, n, s, L) || c >= p.hcap) return;  // block-uniform
+  const int hq = h / (p.H / p.Hg);
+  const bf16* hsrc = reinterpret_cast<const bf16*>(p.h) + (c * p.H + h) * static_cast<int64_t>(K) * V;
+  for (int i = tid; i < K * (V / 8); i += kTh) {
+    const int kr = i / (V / 8), c0 = (i % (V / 8)) * 8;
+    const Vec<bf16, 8> x = *reinterpret_cast<const Vec<bf16, 8>*>(hsrc + kr * V + c0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm.ht[c0 + e][kr] = x.v[e];
+  }
+  const bf16* vsrc = reinterpret_cast<const bf16*>(p.v) + (s * p.H + h) * static_cast<int64_t>(V);
+  for (int i = tid; i < kC * (V / 8); i += kTh) {
+    const int t = i / (V / 8), c0 = (i % (V / 8)) * 8;
+    Vec<bf16, 8> x = *reinterpret_cast<const Vec<bf16, 8>*>(
+        vsrc + static_cast<int64_t>(min(t, L - 1)) * p.H * V + c0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) sm.vt[c0 + e][t] = t < L ? x.v[e] : static_cast<bf16>(0.f);
+  }
+  if (tid < kC) sm.gc[tid] = p.gcum ? p.gcum[(s + min(tid, L - 1)) * p.H + h] : 0.f;
+  __syncthreads();
+
+  const int64_t qrow = static_cast<int64_t>(p.Hg) * K;
+  bf8_t qa[KK];
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+    qa[kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, qrow, wid * 16, kk);
+  // Masked q k^T rows of this wave -> aq (bf16, as the reference's A.to(v)).
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj) {
+    f4_t a = {0.f, 0.f, 0.f, 0.f};
+    if (nj <= wid) {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        a = mfma16(qa[kk], load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, qrow, nj * 16, kk), a);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = wid * 16 + 4 * lg + i, col = nj * 16 + l15;
+      float val = 0.f;
+      if (nj <= wid && row >= col && col < L)
+        val = a[i] * (p.gcum ? safe_exp(sm.gc[row] - sm.gc[col]) : 1.f);
+      sm.aq[row][col] = static_cast<__bf16>(val);
+    }
+  }
+  __builtin_amdgcn_wave_barrier();  // this wave's aq rows are its own
+  bf16* o = reinterpret_cast<bf16*>(p.o);
+#pragma unroll
+  for (int nj = 0; nj < NJ; ++nj) {
+    f4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      acc = mfma16(qa[kk], *reinterpret_cast<const bf8_t*>(&sm.ht[nj * 16 + l15][kk * 32 + 8 * lg]), acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= p.gcum ? __expf(sm.gc[wid * 16 + 4 * lg + i]) : 1.f;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      if (kk * 32 > wid * 16 + 15) continue;  // beyond the diagonal
+      acc = mfma16(*reinterpret_cast<const bf8_t*>(&sm.aq[wid * 16 + l15][kk * 32 + 8 * lg]),
+                   *reinterpret_cast<const bf8_t*>(&sm.vt[nj * 16 + l15][kk * 32 + 8 * lg]), acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = wid * 16 + 4 * lg + i;
+      if (row < L)
+        o[((s + row) * p.H + h) * static_cast<int64_t>(V) + nj * 16 + l15] =
+            from_f32<bf16>(p.scale * acc[i]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side.
+// ---------------------------------------------------------------------------
+int seq_init(Seq& q, const void* cu, xk_dtype cu_dtype, int64_t N, int64_t T, void* ws,
+             size_t ws_bytes, bool need_offsets) {
+  if (N < 0 || T < 0) return XK_ERR_INVALID;
+  if (cu_dtype != XK_I32 && cu_dtype != XK_I64) return XK_ERR_UNSUPPORTED;
+  q.cu = cu;
+  q.cu_i64 = cu_dtype == XK_I64;
+  q.N = N;
+  q.T = T;
+  q.NTmax = T / kC + N;
+  q.chunk_off = nullptr;
+  if (need_offsets) {
+    if (!ws || static_cast<int64_t>(ws_bytes) < align256(4 * (N + 1)) || !aligned(ws, 256))
+      return XK_ERR_WORKSPACE;
+    q.chunk_off = static_cast<int32_t*>(ws);
+  }
+  return XK_OK;
+}
+
+template <class P>
+int launch_offsets(const P& p, hipStream_t s) {
+  hipLaunchKernelGGL(chunk_offsets_kernel<P>, dim3(1), dim3(256), 0, s, p);
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace xk
+
+using namespace xk;
+using namespace xk::gdn;
+
+extern "C" int64_t xk_gdn_stage_workspace_bytes(int64_t num_seqs) {
+  if (num_seqs < 0) return -1;
+  return align256(4 * (num_seqs + 1));
+}
+
+extern "C" int xk_chunk_local_cumsum(const void* g, xk_dtype g_dtype, float* out,
+                                     int64_t total_tokens, int64_t H, const void* cu_seqlens,
+                                     xk_dtype cu_dtype, int64_t N, int64_t chunk_size,
+                                     void* stream) {
+  CumsumParams p{};
+  int st = seq_init(p, cu_seqlens, cu_dtype, N, total_tokens, nullptr, 0, false);
+  if (st) return st;
+  if (H <= 0 || chunk_size <= 0 || (chunk_size & (chunk_size - 1))) return XK_ERR_INVALID;
+  if (total_tokens == 0) return XK_OK;
+  if (!g || !out || !cu_seqlens) return XK_ERR_INVALID;
+  p.g = g;
+  p.out = out;
+  p.H = static_cast<int>(H);
+  p.chunk = static_cast<int>(chunk_size);
+  const int64_t blocks = cdiv(total_tokens * H, kTh);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (g_dtype) {
+    case XK_F32: hipLaunchKernelGGL(chunk_cumsum_kernel<float>, dim3(blocks), dim3(kTh), 0, s, p); break;
+    case XK_BF16: hipLaunchKernelGGL(chunk_cumsum_kernel<bf16>, dim3(blocks), dim3(kTh), 0, s, p); break;
+    case XK_F16: hipLaunchKernelGGL(chunk_cumsum_kernel<f16>, dim3(blocks), dim3(kTh), 0, s, p); break;
+    default: return XK_ERR_UNSUPPORTED;
+  }
+  return launch_status();
+}
+
+extern "C" int xk_chunk_scaled_dot_kkt(const void* k, xk_dtype dtype, const void* beta,
+                                       xk_dtype beta_dtype, const float* g_cumsum, float* A,
+                                       int64_t total_tokens, int64_t Hg, int64_t H, int64_t K,
+                                       const void* cu_seqlens, xk_dtype cu_dtype, int64_t N,
+                                       void* workspace, size_t workspace_bytes, void* stream) {
+  KktParams p{};
+  int st = seq_init(p, cu_seqlens, cu_dtype, N, total_tokens, workspace, workspace_bytes, true);
+  if (st) return st;
+  if (Hg <= 0 || H <= 0 || H % Hg) return XK_ERR_INVALID;
+  if (dtype != XK_BF16 || K != 128) return XK_ERR_UNSUPPORTED;
+  if (beta_dtype != XK_BF16 && beta_dtype != XK_F32) return XK_ERR_UNSUPPORTED;
+  if (N == 0 || total_tokens == 0) return XK_OK;
+  if (!k || !beta || !A || !cu_seqlens || !aligned(k, 16)) return XK_ERR_INVALID;
+  p.k = k;
+  p.beta = beta;
+  p.gcum = g_cumsum;
+  p.A = A;
+  p.H = static_cast<int>(H);
+  p.Hg = static_cast<int>(Hg);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((st = launch_offsets(p, s))) return st;
+  const dim3 grid(p.NTmax, (H + 3) / 4);
+  if (beta_dtype == XK_BF16)
+    hipLaunchKernelGGL((chunk_kkt_kernel<128, bf16>), grid, dim3(kTh), 0, s, p);
+  else
+    hipLaunchKernelGGL((chunk_kkt_kernel<128, float>), grid, dim3(kTh), 0, s, p);
+  return launch_status();
+}
+
+extern "C" int xk_solve_tril(const float* A, void* Ai, xk_dtype ai_dtype, int64_t total_tokens,
+                             int64_t H, const void* cu_seqlens, xk_dtype cu_dtype, int64_t N,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  TrilParams p{};
+  int st = seq_init(p, cu_seqlens, cu_dtype, N, total_tokens, workspace, workspace_bytes, true);
+  if (st) return st;
+  if (H <= 0) return XK_ERR_INVALID;
+  if (!is_float_dtype(ai_dtype)) return XK_ERR_UNSUPPORTED;
+  if (N == 0 || total_tokens == 0) return XK_OK;
+  if (!A || !Ai || !cu_seqlens || !aligned(A, 16)) return XK_ERR_INVALID;
+  p.A = A;
+  p.Ai = Ai;
+  p.H = static_cast<int>(H);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((st = launch_offsets(p, s))) return st;
+  const dim3 grid(p.NTmax, (H + 3) / 4);
+  switch (ai_dtype) {
+    case XK_F32: hipLaunchKernelGGL(solve_tril_kernel<float>, grid, dim3(kTh), 0, s, p); break;
+    case XK_BF16: hipLaunchKernelGGL(solve_tril_kernel<bf16>, grid, dim3(kTh), 0, s, p); break;
+    default: hipLaunchKernelGGL(solve_tril_kernel<f16>, grid, dim3(kTh), 0, s, p); break;
+  }
+  return launch_status();
+}
+
+extern "C" int xk_recompute_w_u(const void* k, const void* v, xk_dtype dtype, const void* beta,
+                                xk_dtype beta_dtype, const float* g_cumsum, const void* Ai,
+                                xk_dtype ai_dtype, void* w, void* u, int64_t total_tokens,
+                                int64_t Hg, int64_t H, int64_t K, int64_t V,
+                                const void* cu_seqlens, xk_dtype cu_dtype, int64_t N,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  WuParams p{};
+  int st = seq_init(p, cu_seqlens, cu_dtype, N, total_tokens, workspace, workspace_bytes, true);
+  if (st) return st;
+  if (Hg <= 0 || H <= 0 || H % Hg) return XK_ERR_INVALID;
+  if (dtype != XK_BF16 || K != 128 || V != 128) return XK_ERR_UNSUPPORTED;
+  if (beta_dtype != XK_BF16 && beta_dtype != XK_F32) return XK_ERR_UNSUPPORTED;
+  if (ai_dtype != XK_BF16 && ai_dtype != XK_F32) return XK_ERR_UNSUPPORTED;
+  if (N == 0 || total_tokens == 0) return XK_OK;
+  if (!k || !v || !beta || !Ai || !w || !u || !cu_seqlens) return XK_ERR_INVALID;
+  if (!aligned(k, 16) || !aligned(v, 16) || !aligned(Ai, 16)) return XK_ERR_INVALID;
+  p.k = k;
+  p.v = v;
+  p.beta = beta;
+  p.gcum = g_cumsum;
+  p.Ai = Ai;
+  p.w = w;
+  p.u = u;
+  p.H = static_cast<int>(H);
+  p.Hg = static_cast<int>(Hg);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((st = launch_offsets(p, s))) return st;
+  const dim3 grid(p.NTmax, H);
+  if (beta_dtype == XK_BF16) {
+    if (ai_dtype == XK_BF16) hipLaunchKernelGGL((recompute_w_u_kernel<bf16, bf16>), grid, dim3(kTh), 0, s, p);
+    else hipLaunchKernelGGL((recompute_w_u_kernel<bf16, float>), grid, dim3(kTh), 0, s, p);
+  } else {
+    if (ai_dtype == XK_BF16) hipLaunchKernelGGL((recompute_w_u_kernel<float, bf16>), grid, dim3(kTh), 0, s, p);
+    else hipLaunchKernelGGL((recompute_w_u_kernel<float, float>), grid, dim3(kTh), 0, s, p);
+  }
+  return launch_status();
+}
+
+extern "C" int xk_chunk_fwd_h(const void* k, const void* w, const void* u, xk_dtype dtype,
+                              const float* g_cumsum, const float* initial_state, void* h,
+                              int64_t num_chunks, void* v_new, float* final_state,
+                              int64_t total_tokens, int64_t Hg, int64_t H, int64_t K, int64_t V,
+                              const void* cu_seqlens, xk_dtype cu_dtype, int64_t N,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  FwdHParams p{};
+  int st = seq_init(p, cu_seqlens, cu_dtype, N, total_tokens, workspace, workspace_bytes, true);
+  if (st) return st;
+  if (Hg <= 0 || H <= 0 || H % Hg || num_chunks < 0) return XK_ERR_INVALID;
+  p.hcap = num_chunks;
+  if (dtype != XK_BF16 || K != 128 || V <= 0 || V % kBV) return XK_ERR_UNSUPPORTED;
+  if (N == 0) return XK_OK;
+  if (!k || !w || !u || !h || !cu_seqlens) return XK_ERR_INVALID;
+  if (!aligned(k, 16) || !aligned(w, 16)) return XK_ERR_INVALID;
+  p.k = k;
+  p.w = w;
+  p.u = u;
+  p.gcum = g_cumsum;
+  p.h0 = initial_state;
+  p.h = h;
+  p.vnew = v_new;
+  p.ht = final_state;
+  p.H = static_cast<int>(H);
+  p.Hg = static_cast<int>(Hg);
+  p.nvt = static_cast<int>(V / kBV);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((st = launch_offsets(p, s))) return st;
+  const int64_t blocks = cdiv(N * H, 8) * 8 * p.nvt;
+  hipLaunchKernelGGL(chunk_fwd_h_kernel<128>, dim3(blocks), dim3(kTh), 0, s, p);
+  return launch_status();
+}
+
+extern "C" int xk_chunk_fwd_o(const void* q, const void* k, const void* v, const void* h,
+                              int64_t num_chunks, xk_dtype dtype, const float* g_cumsum, void* o,
+                              float scale, int64_t total_tokens, int64_t Hg, int64_t H,
+                              int64_t K, int64_t V, const void* cu_seqlens, xk_dtype cu_dtype,
+                              int64_t N, void* workspace, size_t workspace_bytes, void* stream) {
+  FwdOParams p{};
+  int st = seq_init(p, cu_seqlens, cu_dtype, N, total_tokens, workspace, workspace_bytes, true);
+  if (st) return st;
+  if (Hg <= 0 || H <= 0 || H % Hg || num_chunks < 0) return XK_ERR_INVALID;
+  p.hcap = num_chunks;
+  if (dtype != XK_BF16 || K != 128 || V != 128) return XK_ERR_UNSUPPORTED;
+  if (N == 0 || total_tokens == 0) return XK_OK;
+  if (!q || !k || !v || !h || !o || !cu_seqlens) return XK_ERR_INVALID;
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(h, 16))
+    return XK_ERR_INVALID;
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.h = h;
+  p.gcum = g_cumsum;
+  p.o = o;
+  p.scale = scale;
+  p.H = static_cast<int>(H);
+  p.Hg = static_cast<int>(Hg);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((st = launch_offsets(p, s))) return st;
+  hipLaunchKernelGGL((chunk_fwd_o_kernel<128, 128>), dim3(p.NTmax, H), dim3(kTh), 0, s, p);
+  return launch_status();
+}

@@ -449,6 +449,196 @@ def npu_chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
     return o, fin
 
 
+# ---------------------------------------------------------------------------
+# a6b-a6g: the chunked pipeline stage by stage
+# ---------------------------------------------------------------------------
+def _seqs(B: int, T: int, cu_seqlens: Optional[torch.Tensor], dev):
+    """(cu tensor on dev, N): the reference's varlen table, or B sequences
+    of T tokens when cu_seqlens is None (chunk.py's batch convention)."""
+    if cu_seqlens is None:
+        return torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=dev), B
+    cu = cu_seqlens.to(dev).contiguous()
+    if cu.dtype not in (torch.int32, torch.int64):
+        cu = cu.to(torch.int32)
+    return cu, cu.numel() - 1
+
+
+def _num_chunks(cu: torch.Tensor, total: int, chunk: int = 64) -> int:
+    """Chunks of all sequences, with the kernels' clamping of cu_seqlens to
+    [0, total] (the reference's infer_total_chunks, also a host read of
+    cu_seqlens: npu_triton_chunk_gated_delta_rule.cpp:116-138)."""
+    c = cu.detach().to("cpu", torch.int64).clamp(0, total)
+    lens = (c[1:] - c[:-1]).clamp(min=0)
+    return int(((lens + chunk - 1) // chunk).sum())
+
+
+def _stage_ws(N: int, dev) -> torch.Tensor:
+    return torch.empty(max(lib().xk_gdn_stage_workspace_bytes(N), 1),
+                       dtype=torch.uint8, device=dev)
+
+
+def npu_chunk_local_cumsum(g: torch.Tensor, chunk_size: int,
+                           cu_seqlens: Optional[torch.Tensor] = None):
+    """Per-chunk inclusive cumsum of g [B, T, H] along T; fp32 out.
+
+    Mirrors npu_chunk_local_cumsum
+    (triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:151-227);
+    its H <= 64 launch limit (:173-176) does not apply here.
+    """
+    if g.dim() != 3:
+        raise ValueError("chunk_local_cumsum expects g to have shape [B, T, H].")
+    if chunk_size <= 0 or chunk_size & (chunk_size - 1):
+        raise ValueError("chunk_local_cumsum expects chunk_size to be a power of two")
+    B, T, H = g.shape
+    cu, N = _seqs(B, T, cu_seqlens, g.device)
+    gc = g.contiguous()
+    out = torch.empty(g.shape, dtype=torch.float32, device=g.device)
+    st = lib().xk_chunk_local_cumsum(gc.data_ptr(), xk_dtype(gc), out.data_ptr(), B * T, H,
+                                     cu.data_ptr(), xk_dtype(cu), N, chunk_size, _stream(g))
+    check(st, "xk_chunk_local_cumsum")
+    return out
+
+
+def npu_chunk_scaled_dot_kkt_fwd(k: torch.Tensor, beta: torch.Tensor,
+                                 g_cumsum: Optional[torch.Tensor], chunk_size: int = 64,
+                                 cu_seqlens: Optional[torch.Tensor] = None):
+    """A [B, T, H, 64] fp32 = strict_tril(beta_i (k_i . k_j) exp(gc_i - gc_j)).
+
+    Mirrors npu_chunk_scaled_dot_kkt_fwd
+    (triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:229-297).
+    """
+    if chunk_size != 64:
+        raise ValueError("chunk_scaled_dot_kkt_fwd supports chunk_size=64")
+    B, T, Hg, K = k.shape
+    H = beta.size(2)
+    cu, N = _seqs(B, T, cu_seqlens, k.device)
+    kc, bc = k.contiguous(), beta.contiguous()
+    gcum = g_cumsum.to(torch.float32).contiguous() if g_cumsum is not None else None
+    A = torch.empty(B, T, H, 64, dtype=torch.float32, device=k.device)
+    ws = _stage_ws(N, k.device)
+    st = lib().xk_chunk_scaled_dot_kkt(
+        kc.data_ptr(), xk_dtype(kc), bc.data_ptr(), xk_dtype(bc), _ptr(gcum), A.data_ptr(),
+        B * T, Hg, H, K, cu.data_ptr(), xk_dtype(cu), N, ws.data_ptr(), ws.numel(), _stream(k))
+    check(st, "xk_chunk_scaled_dot_kkt")
+    return A
+
+
+def npu_solve_tril(A: torch.Tensor, chunk_size: int = 64,
+                   cu_seqlens: Optional[torch.Tensor] = None,
+                   output_dtype: torch.dtype = torch.float32):
+    """Ai = (I + A)^-1 per chunk, [B, T, H, 64] in output_dtype.
+
+    Mirrors npu_solve_tril
+    (triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:299-395).
+    """
+    if chunk_size != 64:
+        raise ValueError("chunk_gated_delta_rule solve_tril wrapper only supports chunk_size=64.")
+    B, T, H, C = A.shape
+    if C != 64:
+        raise ValueError("solve_tril expects A of shape [B, T, H, 64]")
+    cu, N = _seqs(B, T, cu_seqlens, A.device)
+    Ac = A.to(torch.float32).contiguous()
+    Ai = torch.empty(A.shape, dtype=output_dtype, device=A.device)
+    ws = _stage_ws(N, A.device)
+    st = lib().xk_solve_tril(Ac.data_ptr(), Ai.data_ptr(), xk_dtype(Ai), B * T, H,
+                             cu.data_ptr(), xk_dtype(cu), N, ws.data_ptr(), ws.numel(), _stream(A))
+    check(st, "xk_solve_tril")
+    return Ai
+
+
+def npu_recompute_w_u_fwd(k: torch.Tensor, v: torch.Tensor, beta: torch.Tensor,
+                          g_cumsum: torch.Tensor, A: torch.Tensor,
+                          cu_seqlens: Optional[torch.Tensor] = None):
+    """(w, u) = (Ai (k beta exp(gc)), Ai (v beta)), w like k, u like v.
+
+    Mirrors npu_recompute_w_u_fwd
+    (triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:397-475).
+    """
+    B, T, Hg, K = k.shape
+    H, V = v.size(2), v.size(3)
+    cu, N = _seqs(B, T, cu_seqlens, k.device)
+    kc, vc, bc = k.contiguous(), v.contiguous(), beta.contiguous()
+    gcum = g_cumsum.to(torch.float32).contiguous()
+    Ac = A.contiguous()
+    w = torch.empty(B, T, H, K, dtype=k.dtype, device=k.device)
+    u = torch.empty_like(vc)
+    ws = _stage_ws(N, k.device)
+    st = lib().xk_recompute_w_u(
+        kc.data_ptr(), vc.data_ptr(), xk_dtype(kc), bc.data_ptr(), xk_dtype(bc),
+        gcum.data_ptr(), Ac.data_ptr(), xk_dtype(Ac), w.data_ptr(), u.data_ptr(), B * T, Hg, H,
+        K, V, cu.data_ptr(), xk_dtype(cu), N, ws.data_ptr(), ws.numel(), _stream(k))
+    check(st, "xk_recompute_w_u")
+    return w, u
+
+
+def npu_chunk_gated_delta_rule_fwd_h(k: torch.Tensor, w: torch.Tensor, u: torch.Tensor,
+                                     g: Optional[torch.Tensor] = None,
+                                     initial_state: Optional[torch.Tensor] = None,
+                                     output_final_state: bool = False,
+                                     chunk_size: int = 64, save_new_value: bool = True,
+                                     cu_seqlens: Optional[torch.Tensor] = None,
+                                     chunk_offsets: Optional[torch.Tensor] = None):
+    """Returns (h [B, NT, H, K, V] k-dtype, v_new or None, final_state or None).
+
+    Mirrors npu_chunk_gated_delta_rule_fwd_h
+    (triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:644-802):
+    g is the per-chunk cumsum of the log-decay; h[c] is the state entering
+    chunk c.  chunk_offsets, if given, must match cu_seqlens (the chunk
+    offsets are recomputed on the device).
+    """
+    if chunk_size != 64:
+        raise ValueError("chunk_gated_delta_rule_fwd_h only supports chunk_size=64")
+    for name, t in (("k", k), ("w", w), ("u", u)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"chunk_gated_delta_rule_fwd_h expects {name} to be bfloat16")
+    B, T, Hg, K = k.shape
+    H, V = u.size(2), u.size(3)
+    cu, N = _seqs(B, T, cu_seqlens, k.device)
+    NT = _num_chunks(cu, B * T)
+    if chunk_offsets is not None and chunk_offsets.numel() != N + 1:
+        raise ValueError("chunk_offsets must have N + 1 entries")
+    kc, wc, uc = k.contiguous(), w.contiguous(), u.contiguous()
+    gcum = g.to(torch.float32).contiguous() if g is not None else None
+    h0 = initial_state.to(torch.float32).contiguous() if initial_state is not None else None
+    h = torch.empty(B if cu_seqlens is None else 1, NT // (B if cu_seqlens is None else 1),
+                    H, K, V, dtype=k.dtype, device=k.device)
+    v_new = torch.empty_like(uc) if save_new_value else None
+    fin = torch.empty(N, H, K, V, dtype=torch.float32, device=k.device) if output_final_state else None
+    ws = _stage_ws(N, k.device)
+    st = lib().xk_chunk_fwd_h(
+        kc.data_ptr(), wc.data_ptr(), uc.data_ptr(), xk_dtype(kc), _ptr(gcum), _ptr(h0),
+        h.data_ptr(), NT, _ptr(v_new), _ptr(fin), B * T, Hg, H, K, V, cu.data_ptr(),
+        xk_dtype(cu), N, ws.data_ptr(), ws.numel(), _stream(k))
+    check(st, "xk_chunk_fwd_h")
+    return h, v_new, fin
+
+
+def npu_chunk_fwd_o(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, h: torch.Tensor,
+                    g_cumsum: Optional[torch.Tensor], scale: float, chunk_size: int = 64,
+                    cu_seqlens: Optional[torch.Tensor] = None):
+    """o = scale (exp(gc) (q h_c) + tril(q k^T exp(gc_i - gc_j)) v), like v.
+
+    Mirrors npu_chunk_fwd_o
+    (triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:477-554).
+    """
+    if chunk_size != 64:
+        raise ValueError("chunk_fwd_o supports chunk_size=64")
+    B, T, Hg, K = q.shape
+    H, V = v.size(2), v.size(3)
+    cu, N = _seqs(B, T, cu_seqlens, q.device)
+    qc, kc, vc, hc = q.contiguous(), k.contiguous(), v.contiguous(), h.contiguous()
+    NT = hc.numel() // (H * K * V)
+    gcum = g_cumsum.to(torch.float32).contiguous() if g_cumsum is not None else None
+    o = torch.empty_like(vc)
+    ws = _stage_ws(N, q.device)
+    st = lib().xk_chunk_fwd_o(
+        qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), hc.data_ptr(), NT, xk_dtype(qc),
+        _ptr(gcum), o.data_ptr(), float(scale), B * T, Hg, H, K, V, cu.data_ptr(),
+        xk_dtype(cu), N, ws.data_ptr(), ws.numel(), _stream(q))
+    check(st, "xk_chunk_fwd_o")
+    return o
+
+
 def gdn_conv_decode(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
                     conv_weight: torch.Tensor, g: torch.Tensor,
                     beta: Optional[torch.Tensor], ssm_state: torch.Tensor,
