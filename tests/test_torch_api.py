@@ -1,0 +1,73 @@
+"""The C++ drop-in layer (csrc/torch_api, module _xk_torch) on the CPU: it
+loads, its registry / operation-factory shims map the reference's kernel
+names onto the C-ABI, and its validation raises like the reference wrappers
+before anything touches a GPU."""
+import ctypes
+
+import pytest
+import torch
+
+
+@pytest.fixture(scope="module")
+def xt():
+    from torch_npu_ops_amd import _xk_torch
+    return _xk_torch
+
+
+def test_registry_maps_reference_names_to_entry_points(xt):
+    from torch_npu_ops_amd import _lib
+    lib = _lib.lib()
+    pairs = {
+        "layer_norm_fwd_kernel_fast_rms_bf16_z_nobias_nomask": "xk_layer_norm_fwd",
+        "fused_recurrent_gated_delta_rule_spec_fwd_kernel": "xk_gdn_recurrent",
+        "chunk_gated_delta_rule_fwd_kernel_h_blockdim64": "xk_chunk_fwd_h",
+        "merge_16x16_to_64x64_inverse_kernel": "xk_solve_tril",
+        "_causal_conv1d_update_kernel_npu_tiled_v2": "xk_causal_conv1d_varlen",
+        "split_rmsnorm_rope_kernel": "xk_split_rmsnorm_rope",
+    }
+    for name, sym in pairs.items():
+        assert xt.registry_register(name, "/path/ignored.npubin")
+        assert xt.registry_stub(name) == ctypes.cast(getattr(lib, sym), ctypes.c_void_p).value
+    # kernels outside the op set are not registered
+    assert not xt.registry_register("rope_inplace_kernel", "")
+    assert xt.registry_stub("fused_gdn_gating_decode_kernel") == 0
+
+
+def test_factory_names_and_status_forwarding(xt):
+    assert xt.factory_kernel_name("layer_norm_fwd") == "layer_norm_fwd_kernel"
+    assert xt.factory_kernel_name("chunk_fwd_o") == "chunk_fwd_kernel_o"
+    # execute() returns the C-ABI status of an invalid call (M < 0)
+    assert xt.factory_status_of_invalid_layer_norm() == -1
+
+
+def test_validation_errors_match_reference_messages(xt):
+    x = torch.zeros(4, 12)
+    with pytest.raises(RuntimeError, match="divisible by group_size"):
+        xt.layer_norm_fwd(x, torch.ones(12), torch.zeros(12), 1e-5, None, 5)
+    with pytest.raises(RuntimeError, match="head_first=false"):
+        q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)
+        xt.npu_chunk_gated_delta_rule(q, q, q, torch.zeros(1, 8, 2), torch.zeros(1, 8, 2),
+                                      head_first=True)
+    with pytest.raises(RuntimeError, match="expects q/k/v to be bfloat16"):
+        q = torch.zeros(1, 8, 2, 128)
+        xt.npu_chunk_gated_delta_rule(q, q, q, torch.zeros(1, 8, 2), torch.zeros(1, 8, 2))
+    with pytest.raises(RuntimeError, match="width in \\[1, 6\\]"):
+        xt.npu_causal_conv1d_update_v2(torch.zeros(2, 8), torch.zeros(2, 8, 6),
+                                       torch.zeros(8, 7))
+    with pytest.raises(RuntimeError, match="power of two"):
+        xt.npu_chunk_local_cumsum(torch.zeros(1, 8, 2), 48)
+
+
+def test_cpu_tensors_are_refused(xt):
+    with pytest.raises(RuntimeError, match="GPU device"):
+        xt.layer_norm_fwd(torch.zeros(4, 8), torch.ones(8), torch.zeros(8), 1e-5)
+    with pytest.raises(RuntimeError, match="GPU device"):
+        xt.npu_ops_gemma_rms_norm(torch.zeros(4, 8), torch.ones(8), 1e-6)
+
+
+def test_conv_update_query_start_loc_sentinel(xt):
+    # reference :41-45 warns (TORCH_WARN, c10's log) and returns zeros(1)
+    out = xt.npu_causal_conv1d_update(torch.zeros(2, 8), torch.zeros(2, 8, 3),
+                                      torch.zeros(8, 4),
+                                      query_start_loc=torch.tensor([0, 1, 2]))
+    assert out.shape == (1,) and out.item() == 0

@@ -84,9 +84,68 @@ def build_lib(jobs: int | None = None, verbose: bool = True) -> str:
     return LIB_PATH
 
 
+TORCH_API_DIR = os.path.join(CSRC_DIR, "torch_api")
+TORCH_API_PATH = os.path.join(PKG_DIR, "_xk_torch.so")
+
+
+def torch_api_sources() -> list[str]:
+    return sorted(glob.glob(os.path.join(TORCH_API_DIR, "*.cpp")))
+
+
+def build_torch_api(jobs: int | None = None, verbose: bool = True) -> str:
+    """Compile the C++ drop-in layer (csrc/torch_api) with g++ against the
+    installed PyTorch-ROCm and link _xk_torch.so against libxk.so (found
+    next to it through an $ORIGIN rpath).  Needs libxk.so built first."""
+    import sysconfig
+
+    import torch
+    torch_dir = os.path.dirname(torch.__file__)
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    cxx = os.environ.get("CXX", "g++")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    flags = [
+        "-O2", "-std=c++17", "-fPIC", "-fvisibility=hidden",
+        "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+        "-DTORCH_EXTENSION_NAME=_xk_torch", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+        f"-I{os.path.join(torch_dir, 'include')}",
+        f"-I{os.path.join(torch_dir, 'include', 'torch', 'csrc', 'api', 'include')}",
+        "-I/opt/rocm/include", f"-I{sysconfig.get_paths()['include']}",
+        f"-I{INCLUDE_DIR}", f"-I{TORCH_API_DIR}",
+        "-Wno-deprecated-declarations",
+    ]
+    srcs = torch_api_sources()
+    objs = [os.path.join(BUILD_DIR, "torch_api_" + os.path.basename(s) + ".o") for s in srcs]
+    jobs = jobs or min(8, os.cpu_count() or 4)
+
+    def compile_one(pair):
+        src, obj = pair
+        _run([cxx, *flags, "-c", src, "-o", obj])
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        for obj in ex.map(compile_one, zip(srcs, objs)):
+            if verbose:
+                print(f"[xk build] compiled {os.path.basename(obj)}", flush=True)
+    tmp = TORCH_API_PATH + ".tmp"
+    _run([cxx, "-shared", *objs, "-o", tmp,
+          f"-L{os.path.join(torch_dir, 'lib')}", "-L/opt/rocm/lib",
+          f"-L{PKG_DIR}", "-lxk", "-Wl,-rpath,$ORIGIN",
+          "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip", "-ltorch_hip", "-ltorch_python",
+          "-lamdhip64"])
+    os.replace(tmp, TORCH_API_PATH)
+    if verbose:
+        print(f"[xk build] linked {TORCH_API_PATH}", flush=True)
+    return TORCH_API_PATH
+
+
+def build_all(verbose: bool = True) -> None:
+    build_lib(verbose=verbose)
+    build_torch_api(verbose=verbose)
+
+
 def clean() -> None:
     shutil.rmtree(BUILD_DIR, ignore_errors=True)
 
 
 if __name__ == "__main__":
-    build_lib()
+    build_all()

@@ -1,0 +1,605 @@
+// Implementation of triton_ops_api.h / ascendc_ops_api.h over the C-ABI of
+// libxk.so.  Each function follows the reference wrapper cited beside it
+// (validation, output allocation, in-place state), then calls one xk_*
+// entry point on the current HIP stream and turns a non-zero status into a
+// c10::Error.
+#include "ascendc_ops_api.h"
+#include "triton_ops_api.h"
+
+#include <c10/hip/HIPStream.h>
+
+#include <cmath>
+
+#include "xk_ops.h"
+
+namespace {
+
+xk_dtype xdt(const torch::Tensor& t) {
+  switch (t.scalar_type()) {
+    case torch::kFloat32: return XK_F32;
+    case torch::kBFloat16: return XK_BF16;
+    case torch::kFloat16: return XK_F16;
+    case torch::kInt32: return XK_I32;
+    case torch::kInt64: return XK_I64;
+    default: TORCH_CHECK(false, "unsupported dtype ", t.scalar_type());
+  }
+  return XK_F32;
+}
+
+void* stream_of(const torch::Tensor& t) {
+  TORCH_CHECK(t.is_cuda(), "torch_npu_ops_amd ops need tensors on a GPU device");
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void check(int st, const char* what) {
+  TORCH_CHECK(st == XK_OK, what, " failed: ", xk_status_string(st), " (", st, ")");
+}
+
+template <typename T>
+const void* ptr(const std::optional<T>& t) {
+  return t.has_value() && t->defined() ? t->data_ptr() : nullptr;
+}
+const void* ptr(const torch::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
+void* mptr(torch::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
+
+bool has(const std::optional<torch::Tensor>& t) { return t.has_value() && t->defined(); }
+
+// Row-contiguous 2-D view of x as [-1, N].
+torch::Tensor rows(const torch::Tensor& x, int64_t N) {
+  auto x2 = x.reshape({-1, N});
+  return x2.stride(-1) == 1 ? x2 : x2.contiguous();
+}
+
+// cu_seqlens on the device (int32/int64 kept), or B sequences of T tokens.
+std::pair<torch::Tensor, int64_t> seqs(int64_t B, int64_t T,
+                                       const std::optional<torch::Tensor>& cu_seqlens,
+                                       const torch::Device& dev) {
+  if (!has(cu_seqlens)) {
+    return {torch::arange(0, (B + 1) * T, T, torch::TensorOptions().dtype(torch::kInt32).device(dev)),
+            B};
+  }
+  auto cu = cu_seqlens->to(dev).contiguous();
+  if (cu.scalar_type() != torch::kInt32 && cu.scalar_type() != torch::kInt64)
+    cu = cu.to(torch::kInt32);
+  return {cu, cu.numel() - 1};
+}
+
+// Total chunks of all sequences with the kernels' clamping of cu_seqlens
+// (a host read, as the reference's infer_total_chunks,
+// npu_triton_chunk_gated_delta_rule.cpp:116-138).
+int64_t num_chunks(const torch::Tensor& cu, int64_t total) {
+  auto c = cu.to(torch::kCPU, torch::kInt64).clamp(0, total);
+  auto lens = (c.slice(0, 1) - c.slice(0, 0, -1)).clamp_min(0);
+  return ((lens + 63).div(64, "floor")).sum().item<int64_t>();
+}
+
+torch::Tensor workspace(int64_t bytes, const torch::Device& dev) {
+  return torch::empty({std::max<int64_t>(bytes, 1)},
+                      torch::TensorOptions().dtype(torch::kUInt8).device(dev));
+}
+
+torch::Tensor layer_norm_impl(const torch::Tensor& x, const torch::Tensor& weight,
+                              const torch::Tensor& bias, double eps,
+                              const std::optional<torch::Tensor>& z, int64_t group_size,
+                              bool norm_before_gate, bool is_rms_norm) {
+  TORCH_CHECK(x.dim() >= 1, "layer_norm_fwd expects x.dim() >= 1");
+  const int64_t N = x.size(-1);
+  const int64_t G = group_size > 0 ? group_size : N;
+  TORCH_CHECK(N % G == 0, "x.size(-1) must be divisible by group_size");
+  TORCH_CHECK(weight.defined() && weight.numel() == N, "weight numel must equal x.size(-1)");
+  auto x2 = rows(x, N);
+  torch::Tensor z2;
+  if (has(z)) {
+    TORCH_CHECK(z->sizes() == x.sizes(), "z shape must match x shape");
+    z2 = rows(*z, N);
+  }
+  const int64_t M = x2.size(0);
+  auto w = weight.contiguous();
+  torch::Tensor b;
+  if (bias.defined() && bias.numel() > 0) {  // undefined or empty: no bias
+    TORCH_CHECK(bias.numel() == N, "bias numel must equal x.size(-1)");
+    b = bias.contiguous().to(w.scalar_type());
+  }
+  auto y = torch::empty({M, N}, x.options());
+  const int64_t ng = N / G;
+  // mean / rstd are allocated as the reference does (and not returned).
+  auto f32 = x.options().dtype(torch::kFloat32);
+  torch::Tensor mean = is_rms_norm ? torch::Tensor() : torch::empty({ng * M}, f32);
+  auto rstd = torch::empty({ng * M}, f32);
+  check(xk_layer_norm_fwd(x2.data_ptr(), x2.stride(0), y.data_ptr(), y.stride(0), w.data_ptr(),
+                          ptr(b), ptr(z2), z2.defined() ? z2.stride(0) : 0,
+                          static_cast<float*>(mptr(mean)), static_cast<float*>(rstd.data_ptr()),
+                          M, N, G, static_cast<float>(eps), norm_before_gate,
+                          is_rms_norm, xdt(x), xdt(w), stream_of(x)),
+        "xk_layer_norm_fwd");
+  return y.reshape(x.sizes());
+}
+
+}  // namespace
+
+namespace xllm::kernel::npu {
+
+// triton_npu/torch_api/npu_triton_l2norm.cpp:60-109
+torch::Tensor npu_l2norm_last_dim(torch::Tensor& x, double eps) {
+  TORCH_CHECK(x.dim() >= 1 && x.size(-1) > 0, "npu_l2norm_last_dim expects hidden dim > 0");
+  auto xc = x.contiguous();
+  auto y = torch::empty_like(xc);
+  const int64_t cols = x.size(-1);
+  check(xk_l2norm_last_dim(xc.data_ptr(), y.data_ptr(), xc.numel() / cols, cols,
+                           static_cast<float>(eps), xdt(xc), xdt(y), stream_of(x)),
+        "xk_l2norm_last_dim");
+  return y;
+}
+
+// triton_npu/torch_api/npu_triton_layernorm_fwd.cpp:48-332
+torch::Tensor layer_norm_fwd(torch::Tensor& x, torch::Tensor& weight, torch::Tensor& bias,
+                             double eps, const std::optional<torch::Tensor>& z,
+                             int64_t group_size, bool norm_before_gate, bool is_rms_norm) {
+  return layer_norm_impl(x, weight, bias, eps, z, group_size, norm_before_gate, is_rms_norm);
+}
+
+// triton_npu/torch_api/npu_triton_split_rmsnorm_rope.cpp:56-144
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> npu_split_rmsnorm_rope(
+    torch::Tensor& input, torch::Tensor& sin, torch::Tensor& cos, torch::Tensor& q_weight,
+    torch::Tensor& k_weight, int64_t q_hidden_size, int64_t kv_hidden_size, int64_t head_dim,
+    double eps, const std::optional<torch::Tensor>& q_bias,
+    const std::optional<torch::Tensor>& k_bias, bool bias) {
+  TORCH_CHECK(input.dim() == 2, "split_rmsnorm_rope input must be a 2D tensor");
+  TORCH_CHECK(head_dim > 0 && (head_dim & (head_dim - 1)) == 0,
+              "split_rmsnorm_rope head_dim must be a power of two");
+  TORCH_CHECK(kv_hidden_size > 0 && q_hidden_size % kv_hidden_size == 0,
+              "split_rmsnorm_rope q_hidden_size must be divisible by kv_hidden_size");
+  TORCH_CHECK(kv_hidden_size % head_dim == 0,
+              "split_rmsnorm_rope kv_hidden_size must be divisible by head_dim");
+  TORCH_CHECK(input.size(1) == q_hidden_size + 2 * kv_hidden_size,
+              "split_rmsnorm_rope input hidden size mismatch");
+  TORCH_CHECK(q_weight.numel() == head_dim && k_weight.numel() == head_dim,
+              "split_rmsnorm_rope q/k weight shape mismatch");
+  const int64_t T = input.size(0);
+  TORCH_CHECK(sin.dim() == 2 && cos.dim() == 2 && sin.size(0) == T && cos.size(0) == T &&
+                  sin.size(1) == head_dim && cos.size(1) == head_dim,
+              "split_rmsnorm_rope sin/cos shape mismatch");
+  auto x = input.stride(1) == 1 ? input : input.contiguous();
+  const auto aux = q_weight.scalar_type();
+  auto qw = q_weight.contiguous();
+  auto kw = k_weight.contiguous().to(aux);
+  torch::Tensor qb, kb;
+  if (bias && has(q_bias) && has(k_bias)) {  // reference :109-118
+    qb = q_bias->contiguous().to(aux);
+    kb = k_bias->contiguous().to(aux);
+  }
+  auto s = sin.to(aux).contiguous();
+  auto c = cos.to(aux).contiguous();
+  auto q = torch::empty({T, q_hidden_size}, input.options());
+  auto k = torch::empty({T, kv_hidden_size}, input.options());
+  auto v = torch::empty({T, kv_hidden_size}, input.options());
+  check(xk_split_rmsnorm_rope(x.data_ptr(), x.stride(0), T, s.data_ptr(), c.data_ptr(), head_dim,
+                              nullptr, XK_I64, nullptr, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                              qw.data_ptr(), ptr(qb), kw.data_ptr(), ptr(kb), xdt(qw),
+                              q_hidden_size, kv_hidden_size, head_dim, static_cast<float>(eps),
+                              xdt(x), stream_of(input)),
+        "xk_split_rmsnorm_rope");
+  return {q, k, v};
+}
+
+// triton_npu/torch_api/npu_triton_causal_conv1d_update.cpp:22-138
+torch::Tensor npu_causal_conv1d_update(
+    torch::Tensor& x, torch::Tensor& conv_state, torch::Tensor& weight, bool activation,
+    const std::optional<torch::Tensor>& bias, const std::optional<torch::Tensor>& cache_seqlens,
+    const std::optional<torch::Tensor>& conv_state_indices,
+    const std::optional<torch::Tensor>& num_accepted_tokens,
+    const std::optional<torch::Tensor>& query_start_loc, int32_t /*max_query_len*/,
+    const std::optional<torch::Tensor>& /*intermediate_conv_window*/, int32_t pad_slot_id,
+    bool /*validate_data*/) {
+  if (has(query_start_loc)) {  // reference :41-45
+    TORCH_WARN("npu_causal_conv1d_update does not support query_start_loc");
+    return torch::zeros({1});
+  }
+  TORCH_CHECK(!has(cache_seqlens) && !has(num_accepted_tokens),
+              "causal_conv1d_update does not support cache_seqlens or num_accepted_tokens");
+  const bool unsq = x.dim() == 2;
+  auto xs = unsq ? x.unsqueeze(-1) : x;
+  TORCH_CHECK(xs.dim() == 3, "causal_conv1d_update expects x [B, D] or [B, D, T]");
+  const int64_t B = xs.size(0), D = xs.size(1), T = xs.size(2);
+  const int64_t W = weight.size(1), S = conv_state.size(2);
+  TORCH_CHECK(weight.size(0) == D && conv_state.size(1) == D, "weight / conv_state dim mismatch");
+  auto out = torch::empty_like(xs);
+  torch::Tensor idx;
+  if (has(conv_state_indices)) idx = conv_state_indices->to(torch::kInt32).contiguous();
+  auto w = (weight.scalar_type() == x.scalar_type() || weight.scalar_type() == torch::kFloat32)
+               ? weight
+               : weight.to(x.scalar_type());
+  torch::Tensor b;
+  if (has(bias)) b = bias->to(w.scalar_type()).contiguous();
+  check(xk_causal_conv1d_update(xs.data_ptr(), xs.stride(0), xs.stride(1), xs.stride(2),
+                                conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
+                                conv_state.stride(2), w.data_ptr(), w.stride(0), w.stride(1),
+                                ptr(b), xdt(w), static_cast<const int32_t*>(ptr(idx)),
+                                pad_slot_id, conv_state.size(0), out.data_ptr(), out.stride(0),
+                                out.stride(1), out.stride(2), B, D, T, W, S, activation, xdt(xs),
+                                stream_of(x)),
+        "xk_causal_conv1d_update");
+  return unsq ? out.squeeze(-1) : out;
+}
+
+// triton_npu/torch_api/npu_triton_causal_conv1d_update_v2.cpp:99-239
+torch::Tensor npu_causal_conv1d_update_v2(
+    torch::Tensor& x, torch::Tensor& conv_state, torch::Tensor& weight, bool activation,
+    const std::optional<torch::Tensor>& bias,
+    const std::optional<torch::Tensor>& conv_state_indices,
+    const std::optional<torch::Tensor>& query_start_loc, int32_t max_query_len,
+    int32_t pad_slot_id, const std::optional<torch::Tensor>& block_idx_last_scheduled_token,
+    const std::optional<torch::Tensor>& initial_state_idx, bool /*validate_data*/,
+    const std::optional<torch::Tensor>& num_accepted_tokens) {
+  TORCH_CHECK(weight.dim() == 2, "causal_conv1d_update_v2 expects weight shape [dim, width].");
+  TORCH_CHECK(has(block_idx_last_scheduled_token) == has(initial_state_idx),
+              "causal_conv1d_update_v2 expects both APC tensors or neither.");
+  TORCH_CHECK(conv_state.dim() == 3,
+              "causal_conv1d_update_v2 expects conv_state shape [num_cache_lines, dim, state_len].");
+  const bool dense = !has(query_start_loc);
+  bool unsq = false;
+  int64_t B, D, T = 0, mql;
+  torch::Tensor xt, qsl;
+  if (dense) {
+    unsq = x.dim() == 2;
+    auto xw = unsq ? x.unsqueeze(-1) : x;
+    B = xw.size(0);
+    D = xw.size(1);
+    T = xw.size(2);
+    xt = xw.transpose(1, 2).contiguous().view({B * T, D});
+    qsl = torch::arange(0, (B + 1) * T, T, x.options().dtype(torch::kInt32));
+    mql = T;
+  } else {
+    TORCH_CHECK(x.dim() == 2, "causal_conv1d_update_v2 expects x to be 2D [num_tokens, dim] "
+                              "when query_start_loc is provided.");
+    qsl = query_start_loc->to(torch::kInt32).contiguous();
+    B = qsl.numel() - 1;
+    D = x.size(1);
+    xt = x.stride(1) == 1 ? x : x.contiguous();
+    mql = max_query_len;
+    if (mql < 0)
+      mql = B > 0 ? (qsl.slice(0, 1) - qsl.slice(0, 0, -1)).max().item<int64_t>() : 0;
+  }
+  const int64_t W = weight.size(1);
+  TORCH_CHECK(W >= 1 && W <= 6, "causal_conv1d_update_v2 expects width in [1, 6], got ", W);
+  TORCH_CHECK(weight.size(0) == D && conv_state.size(1) == D, "weight / conv_state dim mismatch");
+  torch::Tensor slots;
+  int64_t sstride = 0;
+  int s2d = 0;
+  if (has(conv_state_indices)) {
+    slots = conv_state_indices->to(torch::kInt32).contiguous();
+    s2d = slots.dim() == 2;
+    sstride = s2d ? slots.stride(0) : 1;
+    TORCH_CHECK(slots.size(0) == B, "conv_state_indices batch mismatch");
+  }
+  torch::Tensor last, init, acc;
+  if (has(block_idx_last_scheduled_token)) {
+    last = block_idx_last_scheduled_token->to(torch::kInt32).contiguous();
+    init = initial_state_idx->to(torch::kInt32).contiguous();
+  }
+  if (has(num_accepted_tokens)) acc = num_accepted_tokens->to(torch::kInt32).contiguous();
+  // x is read in the state's dtype (reference :172), the result returned in
+  // x's own dtype (:238).
+  const auto x_dtype = x.scalar_type();
+  if (xt.scalar_type() != conv_state.scalar_type()) xt = xt.to(conv_state.scalar_type());
+  auto w = (weight.scalar_type() == xt.scalar_type() || weight.scalar_type() == torch::kFloat32)
+               ? weight
+               : weight.to(xt.scalar_type());
+  torch::Tensor b;
+  if (has(bias)) b = bias->to(w.scalar_type()).contiguous();
+  auto out = torch::empty_like(xt);
+  check(xk_causal_conv1d_varlen(
+            xt.data_ptr(), xt.stride(0), xt.size(0), out.data_ptr(), out.stride(0),
+            conv_state.data_ptr(), conv_state.stride(0), conv_state.stride(1),
+            conv_state.stride(2), conv_state.size(0), conv_state.size(2), w.data_ptr(),
+            w.stride(0), w.stride(1), ptr(b), xdt(w),
+            static_cast<const int32_t*>(qsl.data_ptr()), B,
+            static_cast<const int32_t*>(ptr(slots)), sstride, s2d,
+            static_cast<const int32_t*>(ptr(init)), static_cast<const int32_t*>(ptr(last)),
+            static_cast<const int32_t*>(ptr(acc)), D, W, mql, 0, activation, pad_slot_id,
+            xdt(xt), stream_of(x)),
+        "xk_causal_conv1d_varlen");
+  out = out.to(x_dtype);
+  if (dense) {
+    auto o = out.view({B, T, D}).transpose(1, 2);
+    return unsq ? o.squeeze(-1) : o.contiguous();
+  }
+  return out;
+}
+
+// triton_npu/torch_api/npu_triton_recurrent_gated_delta_rule.cpp:54-247
+std::pair<torch::Tensor, torch::Tensor> npu_fused_recurrent_gated_delta_rule(
+    torch::Tensor& q, torch::Tensor& k, torch::Tensor& v, torch::Tensor& g,
+    const std::optional<torch::Tensor>& beta, const std::optional<float>& scale,
+    const std::optional<torch::Tensor>& initial_state, bool inplace_final_state,
+    const std::optional<torch::Tensor>& cu_seqlens,
+    const std::optional<torch::Tensor>& ssm_state_indices,
+    const std::optional<torch::Tensor>& num_accepted_tokens, bool use_qk_l2norm_in_kernel) {
+  const int64_t B = k.size(0), T = k.size(1), H = k.size(2), K = k.size(3);
+  const int64_t HV = v.size(2), V = v.size(3);
+  TORCH_CHECK(has(cu_seqlens) || q.size(0) == 1,
+              "batch size is not 1 when cu_seqlens is not provided");
+  TORCH_CHECK(has(initial_state), "initial_state must be provided");
+  const float sc = scale.has_value() ? *scale : 1.0f / std::sqrt(static_cast<float>(K));
+  const int64_t N = has(cu_seqlens) ? cu_seqlens->numel() - 1 : B;
+  auto qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous(), gc = g.contiguous();
+  torch::Tensor bc;
+  if (has(beta)) bc = beta->contiguous();
+  auto o = torch::empty({B, T, HV, V}, q.options());
+  const torch::Tensor& h0 = *initial_state;
+  TORCH_CHECK(h0.scalar_type() == torch::kFloat32 && h0.is_contiguous(),
+              "initial_state must be contiguous float32");
+  torch::Tensor fin = inplace_final_state
+                          ? h0
+                          : torch::empty({N, HV, K, V}, q.options().dtype(torch::kFloat32));
+  torch::Tensor idx, acc, cu;
+  int64_t s0 = 0, s1 = 0;
+  if (has(ssm_state_indices)) {
+    idx = ssm_state_indices->to(torch::kInt32).contiguous();
+    s0 = idx.stride(0);
+    s1 = idx.dim() == 2 ? idx.stride(1) : 0;
+  }
+  if (has(num_accepted_tokens)) acc = num_accepted_tokens->to(torch::kInt32).contiguous();
+  if (has(cu_seqlens)) cu = cu_seqlens->contiguous();
+  check(xk_gdn_recurrent(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), xdt(qc), gc.data_ptr(),
+                         xdt(gc), ptr(bc), bc.defined() ? xdt(bc) : XK_F32, o.data_ptr(),
+                         static_cast<const float*>(h0.data_ptr()), h0.stride(0),
+                         static_cast<float*>(fin.data_ptr()), fin.stride(0), h0.size(0), ptr(cu),
+                         cu.defined() ? xdt(cu) : XK_I32,
+                         static_cast<const int32_t*>(ptr(idx)), s0, s1,
+                         static_cast<const int32_t*>(ptr(acc)), N, cu.defined() ? 0 : T, H, HV,
+                         K, V, sc, use_qk_l2norm_in_kernel, inplace_final_state, stream_of(q)),
+        "xk_gdn_recurrent");
+  return {o, fin};
+}
+
+// triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:556-642
+std::pair<torch::Tensor, torch::Tensor> npu_chunk_gated_delta_rule(
+    torch::Tensor& q, torch::Tensor& k, torch::Tensor& v, torch::Tensor& g, torch::Tensor& beta,
+    const std::optional<float>& scale, const std::optional<torch::Tensor>& initial_state,
+    bool output_final_state, const std::optional<torch::Tensor>& cu_seqlens, bool head_first,
+    bool use_qk_l2norm_in_kernel) {
+  TORCH_CHECK(!head_first, "chunk_gated_delta_rule torch_api only supports head_first=false.");
+  TORCH_CHECK(q.scalar_type() == torch::kBFloat16 && k.scalar_type() == torch::kBFloat16 &&
+                  v.scalar_type() == torch::kBFloat16,
+              "chunk_gated_delta_rule expects q/k/v to be bfloat16.");
+  const int64_t B = q.size(0), T = q.size(1), H = q.size(2), K = q.size(3);
+  const int64_t HV = v.size(2), V = v.size(3);
+  TORCH_CHECK(q.sizes() == k.sizes(), "q and k must have the same shape.");
+  TORCH_CHECK(HV % H == 0, "chunk_gated_delta_rule expects num_heads_v to be divisible by "
+                           "num_heads_qk, got ", HV, " and ", H);
+  TORCH_CHECK(beta.dim() == 3 && beta.size(0) == B && beta.size(1) == T && beta.size(2) == HV,
+              "beta must have shape [B, T, H].");
+  TORCH_CHECK(g.dim() == 3 && g.size(0) == B && g.size(1) == T && g.size(2) == HV,
+              "g must have shape [B, T, H].");
+  auto [cu, N] = seqs(B, T, cu_seqlens, q.device());
+  const float sc = scale.has_value() ? *scale : std::pow(static_cast<float>(K), -0.5f);
+  auto qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous();
+  auto gc = g.contiguous(), bc = beta.contiguous();
+  torch::Tensor h0;
+  if (has(initial_state)) h0 = initial_state->to(torch::kFloat32).contiguous();
+  auto f32 = q.options().dtype(torch::kFloat32);
+  torch::Tensor fin = output_final_state ? torch::empty({N, HV, K, V}, f32) : torch::Tensor();
+  auto o = torch::empty({B, T, HV, V}, q.options());
+  auto ws = workspace(xk_gdn_chunk_workspace_bytes(B * T, N, HV), q.device());
+  check(xk_gdn_chunk_fwd(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), xdt(qc), gc.data_ptr(),
+                         xdt(gc), bc.data_ptr(), xdt(bc), o.data_ptr(),
+                         static_cast<const float*>(ptr(h0)), static_cast<float*>(mptr(fin)),
+                         cu.data_ptr(), xdt(cu), N, B * T, H, HV, K, V, sc,
+                         use_qk_l2norm_in_kernel, ws.data_ptr(), ws.numel(), stream_of(q)),
+        "xk_gdn_chunk_fwd");
+  return {o, fin};
+}
+
+// triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:151-227
+torch::Tensor npu_chunk_local_cumsum(const torch::Tensor& g, int64_t chunk_size,
+                                     const std::optional<torch::Tensor>& cu_seqlens) {
+  TORCH_CHECK(g.dim() == 3, "chunk_local_cumsum expects g to have shape [B, T, H].");
+  TORCH_CHECK(chunk_size > 0 && (chunk_size & (chunk_size - 1)) == 0,
+              "chunk_local_cumsum expects chunk_size to be a power of two, got ", chunk_size);
+  const int64_t B = g.size(0), T = g.size(1), H = g.size(2);
+  auto [cu, N] = seqs(B, T, cu_seqlens, g.device());
+  auto gc = g.contiguous();
+  auto out = torch::empty(g.sizes(), g.options().dtype(torch::kFloat32));
+  check(xk_chunk_local_cumsum(gc.data_ptr(), xdt(gc), static_cast<float*>(out.data_ptr()),
+                              B * T, H, cu.data_ptr(), xdt(cu), N, chunk_size, stream_of(g)),
+        "xk_chunk_local_cumsum");
+  return out;
+}
+
+// triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:229-297
+torch::Tensor npu_chunk_scaled_dot_kkt_fwd(const torch::Tensor& k, const torch::Tensor& beta,
+                                           const torch::Tensor& g_cumsum, int64_t chunk_size,
+                                           const std::optional<torch::Tensor>& cu_seqlens) {
+  TORCH_CHECK(chunk_size == 64, "chunk_scaled_dot_kkt_fwd supports chunk_size=64");
+  const int64_t B = k.size(0), T = k.size(1), Hg = k.size(2), K = k.size(3), H = beta.size(2);
+  auto [cu, N] = seqs(B, T, cu_seqlens, k.device());
+  auto kc = k.contiguous(), bc = beta.contiguous();
+  torch::Tensor gc;
+  if (g_cumsum.defined()) gc = g_cumsum.to(torch::kFloat32).contiguous();
+  auto A = torch::empty({B, T, H, 64}, k.options().dtype(torch::kFloat32));
+  auto ws = workspace(xk_gdn_stage_workspace_bytes(N), k.device());
+  check(xk_chunk_scaled_dot_kkt(kc.data_ptr(), xdt(kc), bc.data_ptr(), xdt(bc),
+                                static_cast<const float*>(ptr(gc)),
+                                static_cast<float*>(A.data_ptr()), B * T, Hg, H, K,
+                                cu.data_ptr(), xdt(cu), N, ws.data_ptr(), ws.numel(),
+                                stream_of(k)),
+        "xk_chunk_scaled_dot_kkt");
+  return A;
+}
+
+// triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:299-395
+torch::Tensor npu_solve_tril(const torch::Tensor& A, int64_t chunk_size,
+                             const std::optional<torch::Tensor>& cu_seqlens,
+                             torch::ScalarType output_dtype) {
+  TORCH_CHECK(chunk_size == 64,
+              "chunk_gated_delta_rule solve_tril wrapper only supports chunk_size=64.");
+  TORCH_CHECK(A.dim() == 4 && A.size(3) == 64, "solve_tril expects A of shape [B, T, H, 64]");
+  const int64_t B = A.size(0), T = A.size(1), H = A.size(2);
+  auto [cu, N] = seqs(B, T, cu_seqlens, A.device());
+  auto Ac = A.to(torch::kFloat32).contiguous();
+  auto Ai = torch::empty(A.sizes(), A.options().dtype(output_dtype));
+  auto ws = workspace(xk_gdn_stage_workspace_bytes(N), A.device());
+  check(xk_solve_tril(static_cast<const float*>(Ac.data_ptr()), Ai.data_ptr(), xdt(Ai), B * T, H,
+                      cu.data_ptr(), xdt(cu), N, ws.data_ptr(), ws.numel(), stream_of(A)),
+        "xk_solve_tril");
+  return Ai;
+}
+
+// triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:397-475
+std::pair<torch::Tensor, torch::Tensor> npu_recompute_w_u_fwd(
+    const torch::Tensor& k, const torch::Tensor& v, const torch::Tensor& beta,
+    const torch::Tensor& g_cumsum, const torch::Tensor& A,
+    const std::optional<torch::Tensor>& cu_seqlens) {
+  const int64_t B = k.size(0), T = k.size(1), Hg = k.size(2), K = k.size(3);
+  const int64_t H = v.size(2), V = v.size(3);
+  auto [cu, N] = seqs(B, T, cu_seqlens, k.device());
+  auto kc = k.contiguous(), vc = v.contiguous(), bc = beta.contiguous(), Ac = A.contiguous();
+  auto gc = g_cumsum.to(torch::kFloat32).contiguous();
+  auto w = torch::empty({B, T, H, K}, k.options());
+  auto u = torch::empty_like(vc);
+  auto ws = workspace(xk_gdn_stage_workspace_bytes(N), k.device());
+  check(xk_recompute_w_u(kc.data_ptr(), vc.data_ptr(), xdt(kc), bc.data_ptr(), xdt(bc),
+                         static_cast<const float*>(gc.data_ptr()), Ac.data_ptr(), xdt(Ac),
+                         w.data_ptr(), u.data_ptr(), B * T, Hg, H, K, V, cu.data_ptr(), xdt(cu),
+                         N, ws.data_ptr(), ws.numel(), stream_of(k)),
+        "xk_recompute_w_u");
+  return {w, u};
+}
+
+// triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:644-802
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> npu_chunk_gated_delta_rule_fwd_h(
+    torch::Tensor& k, torch::Tensor& w, torch::Tensor& u, const std::optional<torch::Tensor>& g,
+    const std::optional<torch::Tensor>& initial_state, bool output_final_state,
+    int64_t chunk_size, bool save_new_value, const std::optional<torch::Tensor>& cu_seqlens,
+    const std::optional<torch::Tensor>& chunk_offsets) {
+  TORCH_CHECK(chunk_size == 64, "chunk_gated_delta_rule_fwd_h only supports chunk_size=64");
+  TORCH_CHECK(k.scalar_type() == torch::kBFloat16,
+              "chunk_gated_delta_rule_fwd_h expects k to be bfloat16, got ", k.scalar_type());
+  TORCH_CHECK(w.scalar_type() == torch::kBFloat16,
+              "chunk_gated_delta_rule_fwd_h expects w to be bfloat16, got ", w.scalar_type());
+  TORCH_CHECK(u.scalar_type() == torch::kBFloat16,
+              "chunk_gated_delta_rule_fwd_h expects u to be bfloat16, got ", u.scalar_type());
+  const int64_t B = k.size(0), T = k.size(1), Hg = k.size(2), K = k.size(3);
+  const int64_t H = u.size(2), V = u.size(3);
+  auto [cu, N] = seqs(B, T, cu_seqlens, k.device());
+  TORCH_CHECK(!has(chunk_offsets) || chunk_offsets->numel() == N + 1,
+              "chunk_offsets must have N + 1 entries");
+  const int64_t NT = num_chunks(cu, B * T);
+  auto kc = k.contiguous(), wc = w.contiguous(), uc = u.contiguous();
+  torch::Tensor gc, h0;
+  if (has(g)) gc = g->to(torch::kFloat32).contiguous();
+  if (has(initial_state)) h0 = initial_state->to(torch::kFloat32).contiguous();
+  const int64_t hb = has(cu_seqlens) ? 1 : B;
+  auto h = torch::empty({hb, NT / hb, H, K, V}, k.options());
+  torch::Tensor v_new = save_new_value ? torch::empty_like(uc) : torch::Tensor();
+  torch::Tensor fin = output_final_state
+                          ? torch::empty({N, H, K, V}, k.options().dtype(torch::kFloat32))
+                          : torch::Tensor();
+  auto ws = workspace(xk_gdn_stage_workspace_bytes(N), k.device());
+  check(xk_chunk_fwd_h(kc.data_ptr(), wc.data_ptr(), uc.data_ptr(), xdt(kc),
+                       static_cast<const float*>(ptr(gc)), static_cast<const float*>(ptr(h0)),
+                       h.data_ptr(), NT, mptr(v_new), static_cast<float*>(mptr(fin)), B * T, Hg,
+                       H, K, V, cu.data_ptr(), xdt(cu), N, ws.data_ptr(), ws.numel(),
+                       stream_of(k)),
+        "xk_chunk_fwd_h");
+  return {h, v_new, fin};
+}
+
+// triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:477-554
+torch::Tensor npu_chunk_fwd_o(const torch::Tensor& q, const torch::Tensor& k,
+                              const torch::Tensor& v, const torch::Tensor& h,
+                              const torch::Tensor& g_cumsum, float scale, int64_t chunk_size,
+                              const std::optional<torch::Tensor>& cu_seqlens) {
+  TORCH_CHECK(chunk_size == 64, "chunk_fwd_o supports chunk_size=64");
+  const int64_t B = q.size(0), T = q.size(1), Hg = q.size(2), K = q.size(3);
+  const int64_t H = v.size(2), V = v.size(3);
+  auto [cu, N] = seqs(B, T, cu_seqlens, q.device());
+  auto qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous(), hc = h.contiguous();
+  const int64_t NT = hc.numel() / (H * K * V);
+  torch::Tensor gc;
+  if (g_cumsum.defined()) gc = g_cumsum.to(torch::kFloat32).contiguous();
+  auto o = torch::empty_like(vc);
+  auto ws = workspace(xk_gdn_stage_workspace_bytes(N), q.device());
+  check(xk_chunk_fwd_o(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), hc.data_ptr(), NT, xdt(qc),
+                       static_cast<const float*>(ptr(gc)), o.data_ptr(), scale, B * T, Hg, H, K,
+                       V, cu.data_ptr(), xdt(cu), N, ws.data_ptr(), ws.numel(), stream_of(q)),
+        "xk_chunk_fwd_o");
+  return o;
+}
+
+torch::Tensor npu_gdn_conv_decode(
+    torch::Tensor& mixed_qkv, torch::Tensor& conv_state, torch::Tensor& conv_weight,
+    torch::Tensor& g, const std::optional<torch::Tensor>& beta, torch::Tensor& ssm_state,
+    int64_t num_heads_qk, int64_t num_heads_v, int64_t head_k, int64_t head_v,
+    const std::optional<float>& scale, const std::optional<torch::Tensor>& conv_bias,
+    const std::optional<torch::Tensor>& conv_state_indices,
+    const std::optional<torch::Tensor>& ssm_state_indices, int32_t pad_slot_id,
+    bool use_qk_l2norm) {
+  TORCH_CHECK(mixed_qkv.dim() == 2, "gdn_conv_decode expects mixed_qkv [B, D]");
+  const int64_t B = mixed_qkv.size(0), D = mixed_qkv.size(1);
+  TORCH_CHECK(D == 2 * num_heads_qk * head_k + num_heads_v * head_v,
+              "mixed_qkv width does not match the head layout");
+  const float sc = scale.has_value() ? *scale : 1.0f / std::sqrt(static_cast<float>(head_k));
+  auto x = mixed_qkv.stride(1) == 1 ? mixed_qkv : mixed_qkv.contiguous();
+  torch::Tensor cb, ci, si, bc;
+  if (has(conv_bias)) cb = conv_bias->to(conv_weight.scalar_type()).contiguous();
+  if (has(conv_state_indices)) ci = conv_state_indices->to(torch::kInt32).contiguous();
+  if (has(ssm_state_indices)) si = ssm_state_indices->to(torch::kInt32).contiguous();
+  if (has(beta)) bc = beta->contiguous();
+  auto gc = g.contiguous();
+  auto o = torch::empty({B, num_heads_v, head_v}, x.options());
+  check(xk_gdn_conv_decode(x.data_ptr(), x.stride(0), conv_state.data_ptr(), conv_state.stride(0),
+                           conv_state.stride(1), conv_state.stride(2), conv_state.size(0),
+                           conv_state.size(2), conv_weight.data_ptr(), conv_weight.stride(0),
+                           conv_weight.stride(1), ptr(cb), xdt(conv_weight), conv_weight.size(1),
+                           static_cast<const int32_t*>(ptr(ci)), pad_slot_id, gc.data_ptr(),
+                           xdt(gc), ptr(bc), bc.defined() ? xdt(bc) : XK_F32,
+                           static_cast<float*>(ssm_state.data_ptr()), ssm_state.stride(0),
+                           ssm_state.size(0), static_cast<const int32_t*>(ptr(si)),
+                           o.data_ptr(), B, num_heads_qk, num_heads_v, head_k, head_v, sc,
+                           use_qk_l2norm, xdt(x), stream_of(x)),
+        "xk_gdn_conv_decode");
+  return o;
+}
+
+}  // namespace xllm::kernel::npu
+
+namespace npu_ops {
+
+// ascendc_npu/gemma_rms_norm.cpp:28-57
+void npu_gemma_rms_norm(const torch::Tensor& x, const torch::Tensor& gamma, double epsilon,
+                        torch::Tensor& rstdOut, torch::Tensor& yOut) {
+  const int64_t dx = x.dim(), dg = gamma.dim(), N = gamma.numel();
+  TORCH_CHECK(dx >= dg && x.sizes().slice(dx - dg) == gamma.sizes(),
+              "gamma shape must match the trailing dims of x");
+  std::vector<int64_t> rshape;
+  if (dx > dg) {
+    for (int64_t i = 0; i < dx - dg; ++i) rshape.push_back(x.size(i));
+    for (int64_t i = 0; i < dg; ++i) rshape.push_back(1);
+  } else {
+    rshape.assign(dx, 1);
+  }
+  auto x2 = rows(x, N);
+  auto y = torch::empty_like(x2);
+  auto rstd = torch::empty(rshape, x.options().dtype(torch::kFloat32));
+  auto gm = gamma.contiguous();
+  check(xk_gemma_rms_norm(x2.data_ptr(), x2.stride(0), y.data_ptr(), y.stride(0), gm.data_ptr(),
+                          static_cast<float*>(rstd.data_ptr()), x2.size(0), N,
+                          static_cast<float>(epsilon), xdt(x), xdt(gm), stream_of(x)),
+        "xk_gemma_rms_norm");
+  yOut = y.reshape(x.sizes());
+  rstdOut = rstd;
+}
+
+// ascendc_npu/layer_norm_fwd.cpp:24-80
+torch::Tensor layer_norm_fwd(const torch::Tensor& x, const torch::Tensor& weight,
+                             const c10::optional<torch::Tensor>& bias, double eps,
+                             const c10::optional<torch::Tensor>& z, int64_t group_size,
+                             bool norm_before_gate, bool is_rms_norm) {
+  torch::Tensor b;
+  if (bias.has_value() && bias->defined()) b = *bias;
+  return layer_norm_impl(x, weight, b, eps, z, group_size, norm_before_gate, is_rms_norm);
+}
+
+}  // namespace npu_ops
