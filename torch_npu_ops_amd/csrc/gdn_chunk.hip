@@ -71,6 +71,7 @@ struct ChunkParams {
   const void* cu;   // [N+1]
   int cu_i64;
   int32_t* chunk_off;  // [N+1] workspace
+  int32_t* seq_order;  // [N] workspace: sequences, longest first
   bf16* dump;          // [64 * 32] workspace: sink for padded-row stores
   char* rec;           // [NTmax, HV] records of kRec bytes, workspace
   int64_t N, NTmax;
@@ -267,24 +268,29 @@ struct __align__(16) P2Smem {
   __bf16 dt[2][kBV][kLt];     // (ed * Vn) transposed, hi / lo
 };
 
-// Operands one lane reads from global memory for one chunk, in two groups:
-// those the chunk consumes first (double-buffered: loaded a whole chunk
-// ahead) and those it consumes late (one buffer, reloaded for the next chunk
-// once the current one is done with them), which keeps two waves per SIMD.
+// Operands one lane reads from global memory for one chunk, in three
+// groups.  Those the chunk consumes first are double-buffered (loaded a whole
+// chunk ahead).  The two later groups have one buffer each, refilled with
+// the next chunk's operands right after their last use in the current chunk
+// (so each load has most of a chunk to land) -- this keeps two waves per
+// SIMD.
 template <int KK>
 struct EarlyOps {
   bf8_t kA[KK];          // K rows wid*16 + l15 (A operands)
   bf16 v[2][4];          // v at the lane's C-layout positions (raw: converting
                          // at load time would stall on the load)
   f4_t ck, bt;           // factors of rows wid*16 + 4*lg + i
+  float egl;             // exp(gc_last)
+};
+struct InvOps {          // consumed by Vn = Ai R and ed * Vn
+  bf8_t aiH[2], aiL[2];  // Ai rows wid*16 + l15, hi / lo
+  f4_t ed;
 };
 template <int KK>
-struct LateOps {
-  bf8_t qA[KK];          // Q rows wid*16 + l15 (Q S only feeds the output)
-  bf8_t aiH[2], aiL[2];  // Ai rows wid*16 + l15, hi / lo
+struct OutOps {          // consumed by the output o = cq (Q S) + Aq Vn
+  bf8_t qA[KK];          // Q rows wid*16 + l15
   bf8_t aq[2];           // Aq rows wid*16 + l15
-  f4_t cq, ed;
-  float egl;             // exp(gc_last)
+  f4_t cq;
 };
 
 // Token row of q/k/v for C-layout row `r` (rows >= L read row L-1: finite,
@@ -315,11 +321,29 @@ __device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32
   const int r4 = wid * 16 + 4 * lg;
   ops.ck = *reinterpret_cast<const f4_t*>(sc + 1 * kC + r4);
   ops.bt = *reinterpret_cast<const f4_t*>(sc + 2 * kC + r4);
+  ops.egl = sc[4 * kC];
+}
+
+__device__ __forceinline__ void load_inv(const ChunkParams& p, InvOps& ops, int64_t cidx,
+                                         int hv) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int l15 = lane & 15, lg = lane >> 4;
+  const char* rec = rec_at(p, cidx, hv);
+  const __bf16* aih = reinterpret_cast<const __bf16*>(rec);
+  const __bf16* ail = reinterpret_cast<const __bf16*>(rec + kMat);
+  const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int off = (wid * 16 + l15) * kC + kk * 32 + 8 * lg;
+    ops.aiH[kk] = *reinterpret_cast<const bf8_t*>(aih + off);
+    ops.aiL[kk] = *reinterpret_cast<const bf8_t*>(ail + off);
+  }
+  ops.ed = *reinterpret_cast<const f4_t*>(sc + 3 * kC + wid * 16 + 4 * lg);
 }
 
 template <int K>
-__device__ __forceinline__ void load_late(const ChunkParams& p, LateOps<K / 32>& ops,
-                                          int64_t s, int L, int64_t cidx, int hv, int hq) {
+__device__ __forceinline__ void load_out(const ChunkParams& p, OutOps<K / 32>& ops, int64_t s,
+                                         int L, int64_t cidx, int hv, int hq) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int l15 = lane & 15, lg = lane >> 4;
   const uint32_t rs = static_cast<uint32_t>(p.H) * K;
@@ -328,21 +352,12 @@ __device__ __forceinline__ void load_late(const ChunkParams& p, LateOps<K / 32>&
 #pragma unroll
   for (int kk = 0; kk < K / 32; ++kk) ops.qA[kk] = *reinterpret_cast<const bf8_t*>(qp + kk * 32);
   const char* rec = rec_at(p, cidx, hv);
-  const __bf16* aih = reinterpret_cast<const __bf16*>(rec);
-  const __bf16* ail = reinterpret_cast<const __bf16*>(rec + kMat);
   const __bf16* aqp = reinterpret_cast<const __bf16*>(rec + 2 * kMat);
   const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const int off = (wid * 16 + l15) * kC + kk * 32 + 8 * lg;
-    ops.aiH[kk] = *reinterpret_cast<const bf8_t*>(aih + off);
-    ops.aiL[kk] = *reinterpret_cast<const bf8_t*>(ail + off);
-    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + off);
-  }
-  const int r4 = wid * 16 + 4 * lg;
-  ops.cq = *reinterpret_cast<const f4_t*>(sc + 0 * kC + r4);
-  ops.ed = *reinterpret_cast<const f4_t*>(sc + 3 * kC + r4);
-  ops.egl = sc[4 * kC];
+  for (int kk = 0; kk < 2; ++kk)
+    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + (wid * 16 + l15) * kC + kk * 32 + 8 * lg);
+  ops.cq = *reinterpret_cast<const f4_t*>(sc + 0 * kC + wid * 16 + 4 * lg);
 }
 
 // K rows of the lane's A operands written transposed: kt[k][token].
@@ -368,12 +383,14 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   const int l15 = lane & 15, lg = lane >> 4;
   // XCD-aware mapping: the nvt V tiles of one (sequence, head) get block ids
   // that are equal modulo 8, i.e. run on the same XCD and share its L2.
+  // Items are dispatched longest sequence first, so the longest chains start
+  // in the first wave of resident blocks.
   const int64_t w = blockIdx.x;
   const int64_t xcd = w & 7, r = w >> 3;
   const int vt = static_cast<int>(r % nvt);
-  const int64_t item = (r / nvt) * 8 + xcd;  // (sequence, head) index
+  const int64_t item = (r / nvt) * 8 + xcd;  // (sequence rank, head) index
   if (item >= p.N * p.HV) return;            // whole block
-  const int64_t n = item / p.HV;
+  const int64_t n = p.seq_order[item / p.HV];
   const int hv = static_cast<int>(item % p.HV);
   const int hq = hv / (p.HV / p.H);
   const int V = nvt * kBV;
@@ -414,19 +431,22 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   const uint32_t vrow = static_cast<uint32_t>(p.HV) * V;  // v / o token stride
   const int vcol0 = hv * V + v0;
   EarlyOps<KK> opsA, opsB;
-  LateOps<KK> late;
+  InvOps inv;
+  OutOps<KK> outo;
   if (nch > 0) {
     const int L0 = static_cast<int>(min<int64_t>(kC, eos - bos));
     load_early<K>(p, opsA, bos, L0, cidx0, hv, hq, vrow, vcol0);
-    load_late<K>(p, late, bos, L0, cidx0, hv, hq);
+    load_inv(p, inv, cidx0, hv);
+    load_out<K>(p, outo, bos, L0, cidx0, hv, hq);
     store_kt<K>(sm.kt[0], opsA.kA);
   }
   __syncthreads();
 
   // One chunk: `cur` holds its early operands, `nxt` receives the next
-  // chunk's; `late` is reloaded for the next chunk at the end.
-  // The last chunk "prefetches" itself again (unused), so that every memory
-  // operation of the loop is unconditional.
+  // chunk's; `inv` and `outo` are refilled with the next chunk's operands
+  // right after their last use here.  The last chunk "prefetches" itself
+  // again (unused), so that every memory operation of the loop is
+  // unconditional.
   auto step = [&](const EarlyOps<KK>& cur, EarlyOps<KK>& nxt, int64_t ci) {
     const int64_t s = bos + ci * kC;
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
@@ -471,7 +491,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       for (int kk = 0; kk < 2; ++kk) {
         const bf8_t rh = *reinterpret_cast<const bf8_t*>(&sm.rt[0][nj * 16 + l15][kk * 32 + 8 * lg]);
         const bf8_t rl = *reinterpret_cast<const bf8_t*>(&sm.rt[1][nj * 16 + l15][kk * 32 + 8 * lg]);
-        vn[nj] = mfma_split3(late.aiH[kk], late.aiL[kk], rh, rl, vn[nj]);
+        vn[nj] = mfma_split3(inv.aiH[kk], inv.aiL[kk], rh, rl, vn[nj]);
       }
     }
     // Vn -> vt (bf16), ed * Vn -> dt (hi / lo).
@@ -481,32 +501,38 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         b.v[i] = static_cast<__bf16>(vn[nj][i]);
-        split(late.ed[i] * vn[nj][i], h.v[i], l.v[i]);
+        split(inv.ed[i] * vn[nj][i], h.v[i], l.v[i]);
       }
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.vt[nj * 16 + l15][wid * 16 + 4 * lg]) = b;
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = h;
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = l;
     }
-    __syncthreads();  // (2) vt, dt complete; rt reads done
-
-    // o = cq (Q S) + Aq Vn, Q S with the hi part of S (sb is rewritten only
-    // after this).
+    load_inv(p, inv, cidx0 + cn, hv);  // this chunk is done with `inv`
+    // Q S with the hi part of S.  It must read sb before barrier 2: after it,
+    // a wave that is ahead may already publish the next state into sb.
+    f4_t qs[2];
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj) {
-      f4_t qs = {0.f, 0.f, 0.f, 0.f};
+      qs[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
-        qs = mfma16(late.qA[kk], sh, qs);
+        qs[nj] = mfma16(outo.qA[kk], sh, qs[nj]);
       }
+    }
+    __syncthreads();  // (2) vt, dt complete; rt and sb reads done
+
+    // o = cq (Q S) + Aq Vn.
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
       f4_t acc;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = late.cq[i] * qs[i];
+      for (int i = 0; i < 4; ++i) acc[i] = outo.cq[i] * qs[nj][i];
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         if (kk * 32 > wid * 16 + 15) continue;  // Aq columns beyond the diagonal
         const bf8_t vb = *reinterpret_cast<const bf8_t*>(&sm.vt[nj * 16 + l15][kk * 32 + 8 * lg]);
-        acc = mfma16(late.aq[kk], vb, acc);
+        acc = mfma16(outo.aq[kk], vb, acc);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -517,9 +543,10 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
         *dst = from_f32<T>(acc[i]);
       }
     }
+    load_out<K>(p, outo, sn, Ln, cidx0 + cn, hv, hq);  // this chunk is done with `outo`
 
     // S <- exp(gc_last) S + K^T (ed Vn) on the wave's register rows, then
-    // its bf16 copy (every wave finished reading sb before barrier 1).
+    // its bf16 copy (every wave finished reading sb before barrier 2).
     const __bf16 (*kt)[kLt] = sm.kt[ci & 1];
 #pragma unroll
     for (int m2 = 0; m2 < M2; ++m2) {
@@ -532,7 +559,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       for (int nj = 0; nj < 2; ++nj) {
         f4_t acc = sreg[m2][nj];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] *= late.egl;
+        for (int i = 0; i < 4; ++i) acc[i] *= cur.egl;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const bf8_t dh = *reinterpret_cast<const bf8_t*>(&sm.dt[0][nj * 16 + l15][kk * 32 + 8 * lg]);
@@ -544,7 +571,6 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       }
     }
     publish_state();
-    load_late<K>(p, late, sn, Ln, cidx0 + cn, hv, hq);  // this chunk is done with `late`
     store_kt<K>(sm.kt[(ci + 1) & 1], nxt.kA);
     __syncthreads();  // (3) state copy, next keys complete; vt / dt / kt reads done
   };
@@ -568,7 +594,8 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 
 template <int K, typename GT, typename BT>
 int launch_chunk(const ChunkParams& p, int64_t V, hipStream_t s) {
-  hipLaunchKernelGGL(chunk_offsets_kernel<ChunkParams>, dim3(1), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(chunk_offsets_kernel<ChunkParams>, dim3(1), dim3(256), 0, s, p,
+                     p.seq_order);
   int st = launch_status();
   if (st) return st;
   hipLaunchKernelGGL((gdn_chunk_prep_kernel<K, GT, BT>), dim3(p.NTmax, (p.HV + 3) / 4),
@@ -601,7 +628,8 @@ using namespace xk;
 extern "C" int64_t xk_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t num_seqs,
                                                 int64_t HV) {
   if (total_tokens < 0 || num_seqs < 0 || HV <= 0) return -1;
-  return align256(4 * (num_seqs + 1)) + kDump + nt_max(total_tokens, num_seqs) * HV * kRec;
+  return align256(4 * (num_seqs + 1)) + align256(4 * num_seqs) + kDump +
+         nt_max(total_tokens, num_seqs) * HV * kRec;
 }
 
 extern "C" int xk_gdn_chunk_fwd(
@@ -636,9 +664,13 @@ extern "C" int xk_gdn_chunk_fwd(
   p.ht = final_state;
   p.cu = cu_seqlens;
   p.cu_i64 = cu_dtype == XK_I64;
-  p.chunk_off = static_cast<int32_t*>(workspace);
-  p.dump = reinterpret_cast<bf16*>(static_cast<char*>(workspace) + align256(4 * (N + 1)));
-  p.rec = static_cast<char*>(workspace) + align256(4 * (N + 1)) + kDump;
+  char* ws = static_cast<char*>(workspace);
+  p.chunk_off = reinterpret_cast<int32_t*>(ws);
+  ws += align256(4 * (N + 1));
+  p.seq_order = reinterpret_cast<int32_t*>(ws);
+  ws += align256(4 * N);
+  p.dump = reinterpret_cast<bf16*>(ws);
+  p.rec = ws + kDump;
   p.N = N;
   p.NTmax = nt_max(total_tokens, N);
   p.T = total_tokens;

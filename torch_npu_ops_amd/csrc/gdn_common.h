@@ -77,20 +77,31 @@ __device__ __forceinline__ int64_t cu_at(const P& p, int64_t i) {
   return min(max(v, int64_t{0}), p.T);
 }
 
-// chunk_off[n] = sum_{m<n} ceil(len_m / 64), chunk_off[N] = total chunks.
-// One block of 256 threads.
+// Chunks of sequence n (ceil(len / 64); 0 for an empty sequence).
 template <class P>
-__global__ void __launch_bounds__(256) chunk_offsets_kernel(P p) {
+__device__ __forceinline__ int32_t seq_chunks(const P& p, int64_t n) {
+  const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
+  return static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+}
+
+// Sequences whose count is at most this are ranked longest-first by
+// chunk_offsets_kernel (an O(N^2 / 256) ranking); longer lists keep their
+// own order.
+constexpr int64_t kSortMaxSeqs = 2048;
+
+// chunk_off[n] = sum_{m<n} ceil(len_m / 64), chunk_off[N] = total chunks.
+// If `order` is given, order[r] = the sequence of rank r when sequences are
+// sorted by chunk count, longest first (ties by index), or order[r] = r for
+// more than kSortMaxSeqs sequences.  One block of 256 threads.
+template <class P>
+__global__ void __launch_bounds__(256) chunk_offsets_kernel(P p, int32_t* order) {
   constexpr int kT = 256;
   __shared__ int32_t part[kT];
   const int tid = threadIdx.x;
   const int64_t per = (p.N + kT - 1) / kT;
   const int64_t b0 = tid * per, b1 = min(p.N, b0 + per);
   int32_t s = 0;
-  for (int64_t n = b0; n < b1; ++n) {
-    const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
-    s += static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
-  }
+  for (int64_t n = b0; n < b1; ++n) s += seq_chunks(p, n);
   part[tid] = s;
   __syncthreads();
   if (tid == 0) {
@@ -105,10 +116,24 @@ __global__ void __launch_bounds__(256) chunk_offsets_kernel(P p) {
   int32_t acc = part[tid];
   for (int64_t n = b0; n < b1; ++n) {
     p.chunk_off[n] = acc;
-    const int64_t len = cu_at(p, n + 1) - cu_at(p, n);
-    acc += static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+    acc += seq_chunks(p, n);
   }
   if (tid == kT - 1) p.chunk_off[p.N] = acc;
+  if (!order) return;
+  // Ranks are a permutation of [0, N): distinct (chunks, index) keys.
+  const bool sort = p.N <= kSortMaxSeqs;
+  for (int64_t n = tid; n < p.N; n += kT) {
+    int64_t rank = n;
+    if (sort) {
+      const int32_t cn = seq_chunks(p, n);
+      rank = 0;
+      for (int64_t m = 0; m < p.N; ++m) {
+        const int32_t cm = seq_chunks(p, m);
+        rank += (cm > cn) || (cm == cn && m < n);
+      }
+    }
+    order[rank] = static_cast<int32_t>(n);
+  }
 }
 
 // Global chunk c -> sequence n, first token s, length L (1..64); false if c

@@ -569,7 +569,7 @@ int seq_init(Seq& q, const void* cu, xk_dtype cu_dtype, int64_t N, int64_t T, vo
 
 template <class P>
 int launch_offsets(const P& p, hipStream_t s) {
-  hipLaunchKernelGGL(chunk_offsets_kernel<P>, dim3(1), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(chunk_offsets_kernel<P>, dim3(1), dim3(256), 0, s, p, nullptr);
   return launch_status();
 }
 
