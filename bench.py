@@ -4,11 +4,13 @@
     python bench.py [--steps K] [--warmup W] [--op NAME] [--no-cpu] [--eager]
 
 One step = one call of an op on its BASELINE config with inputs already
-resident in HBM.  The K timed calls are captured in one HIP graph and
-replayed back to back (launch overhead of the Python binding would
-otherwise dominate the microsecond-scale ops); HIP events on the stream the
-kernels run on bracket the replay.  Inputs rotate over several buffer sets
-whose total exceeds the 256 MB Infinity Cache, so timings see HBM.
+resident in HBM.  HIP events on the stream the kernels run on bracket the K
+timed calls, launched back to back.  Ops that move >= 100 MB per call are
+launched eagerly (the GPU queue stays ahead of the Python binding); the two
+microsecond-scale ops (configs 1 and 3b), whose kernels are shorter than a
+Python launch, are captured in one HIP graph that is replayed.  Inputs
+rotate over several buffer sets whose total exceeds the 256 MB Infinity
+Cache, so timings see HBM.
 
 Rank 0 prints ONE JSON line:
   value        achieved GB/s of the headline op (algorithmic bytes / time)
@@ -62,6 +64,7 @@ class Case:
     config = ""
     kernel = ""
     algo_bytes = 0
+    timing = "eager"  # or "graph" for ops shorter than a Python launch
 
     def sets(self, dev, n):
         raise NotImplementedError
@@ -156,6 +159,7 @@ class RopeCase(Case):
               "8 kv heads, head_dim 128, eps 1e-6, theta 1e6, sin/cos rows from "
               "positions U[0,4096)")
     kernel = "split_rmsnorm_rope_kernel"
+    timing = "graph"
     T, HQ, HKV, HD = 256, 32, 8, 128
     # qkv in + q/k/v out (fp32) + q/k weights + sin/cos rows
     algo_bytes = (T * (HQ + 2 * HKV) * HD * 4 * 2 + 2 * HD * 4 + 2 * T * HD * 4)
@@ -272,6 +276,7 @@ class ConvDecodeCase(Case):
     config = ("config 3b: causal_conv1d decode update bf16, batch 256 x dim 8192, "
               "conv_state [256,8192,3] ~N(0,1), width 4, SiLU, indices arange")
     kernel = "conv1d_update_w4_kernel"
+    timing = "graph"
     B, D, W = 256, 8192, 4
     algo_bytes = B * D * 2 * 2 + B * D * (W - 1) * 2 * 2 + D * W * 2
 
@@ -514,6 +519,8 @@ HEADLINE = "layer_norm_fwd"
 # Timing
 # ---------------------------------------------------------------------------
 def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
+    """Mean per-call time (ms) of `steps` back-to-back calls, median of
+    three timed repetitions."""
     per_set = max(case.algo_bytes, 1)
     nsets = max(2, min(MAX_SETS, -(-ROTATE_BYTES // per_set)))
     runs = case.sets(dev, nsets)
@@ -527,12 +534,15 @@ def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     if eager:
-        t0.record()
-        for i in range(steps):
-            runs[i % nsets]()
-        t1.record()
-        torch.cuda.synchronize()
-        ms = t0.elapsed_time(t1) / steps
+        reps = []
+        for _ in range(3):
+            t0.record()
+            for i in range(steps):
+                runs[i % nsets]()
+            t1.record()
+            torch.cuda.synchronize()
+            reps.append(t0.elapsed_time(t1) / steps)
+        ms = statistics.median(reps)
     else:
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
@@ -594,7 +604,9 @@ def main():
     ap.add_argument("--op", default=None, help="time only this op")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true",
-                    help="time eager launches instead of a graph replay")
+                    help="time every op with eager launches")
+    ap.add_argument("--graph", action="store_true",
+                    help="time every op with a HIP graph replay")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run plain 256 MiB device copies (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -616,11 +628,13 @@ def main():
     ops = {}
     for name in names:
         case = CASES[name]()
-        ms = time_gpu(case, dev, args.steps, args.warmup, args.eager)
+        eager = args.eager or (case.timing == "eager" and not args.graph)
+        ms = time_gpu(case, dev, args.steps, args.warmup, eager)
         gbs = case.algo_bytes / (ms * 1e-3) / 1e9
         ops[name] = {
             "config": case.config,
             "kernel": case.kernel,
+            "timing": "eager" if eager else "graph",
             "us_per_call": round(ms * 1e3, 2),
             "algo_bytes": case.algo_bytes,
             "GB/s": round(gbs, 1),

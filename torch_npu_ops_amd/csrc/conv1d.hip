@@ -47,10 +47,16 @@ __device__ __forceinline__ float act(float v, int silu_on) {
 // Decode update, width 4 / state_len 3 / one token, contiguous layout:
 // x, out [B, D]; state [lines, D, 3]; weight [D, 4].  One lane owns 8
 // channels: 48 contiguous bytes of state (3 x 16 B), 16 B of x, 64 B of
-// weights, and writes 16 B of output plus 48 B of state.
+// weights, and writes 16 B of output plus 48 B of state.  The x and weight
+// loads are issued before the slot lookup, so their latency overlaps the
+// dependent index -> state chain; x, out and the state move with
+// non-temporal accesses (read once, written once).  Small blocks (one wave)
+// spread the short-lived work evenly over the CUs.
 // ---------------------------------------------------------------------------
+constexpr int kW4Block = 64;
+
 template <typename T, typename WT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(kW4Block)
     conv1d_update_w4_kernel(const T* __restrict__ x, T* __restrict__ out,
                             T* __restrict__ state, int64_t state_line_stride,
                             const WT* __restrict__ w, xk_dtype wdt,
@@ -59,20 +65,20 @@ __global__ void __launch_bounds__(256)
                             int64_t lines, int64_t B, int64_t D, int silu_on) {
   constexpr int kC = 8;
   const int64_t b = blockIdx.y;
-  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * kC;
+  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * kW4Block + threadIdx.x) * kC;
   if (c0 >= D) return;
+  using V8 = Vec<T, kC>;
+  const V8 xv = ld_stream(reinterpret_cast<const V8*>(x + b * D + c0));
+  // The 8 channels' 4 taps are 32 contiguous weights.
+  const Vec<WT, 32> wv = *reinterpret_cast<const Vec<WT, 32>*>(w + c0 * 4);
   const int64_t slot = idx ? idx[b] : b;
   if ((idx && slot == pad) || slot < 0 || slot >= lines) return;
   T* st = state + slot * state_line_stride + c0 * 3;
-  using V8 = Vec<T, kC>;
   // 24 state values (channel-major: s[c*3 + k]) as three 8-element vectors.
   Arr<T, 24> s;
-  *reinterpret_cast<V8*>(&s.v[0]) = reinterpret_cast<const V8*>(st)[0];
-  *reinterpret_cast<V8*>(&s.v[8]) = reinterpret_cast<const V8*>(st)[1];
-  *reinterpret_cast<V8*>(&s.v[16]) = reinterpret_cast<const V8*>(st)[2];
-  const V8 xv = *reinterpret_cast<const V8*>(x + b * D + c0);
-  // The 8 channels' 4 taps are 32 contiguous weights.
-  const Vec<WT, 32> wv = *reinterpret_cast<const Vec<WT, 32>*>(w + c0 * 4);
+  *reinterpret_cast<V8*>(&s.v[0]) = ld_stream(reinterpret_cast<const V8*>(st));
+  *reinterpret_cast<V8*>(&s.v[8]) = ld_stream(reinterpret_cast<const V8*>(st) + 1);
+  *reinterpret_cast<V8*>(&s.v[16]) = ld_stream(reinterpret_cast<const V8*>(st) + 2);
   V8 ov;
   Arr<T, 24> ns;
 #pragma unroll
@@ -92,10 +98,10 @@ __global__ void __launch_bounds__(256)
     ns.v[c * 3 + 1] = s.v[c * 3 + 2];
     ns.v[c * 3 + 2] = xv.v[c];
   }
-  *reinterpret_cast<V8*>(out + b * D + c0) = ov;
-  reinterpret_cast<V8*>(st)[0] = *reinterpret_cast<const V8*>(&ns.v[0]);
-  reinterpret_cast<V8*>(st)[1] = *reinterpret_cast<const V8*>(&ns.v[8]);
-  reinterpret_cast<V8*>(st)[2] = *reinterpret_cast<const V8*>(&ns.v[16]);
+  st_stream(reinterpret_cast<V8*>(out + b * D + c0), ov);
+  st_stream(reinterpret_cast<V8*>(st), *reinterpret_cast<const V8*>(&ns.v[0]));
+  st_stream(reinterpret_cast<V8*>(st) + 1, *reinterpret_cast<const V8*>(&ns.v[8]));
+  st_stream(reinterpret_cast<V8*>(st) + 2, *reinterpret_cast<const V8*>(&ns.v[16]));
 }
 
 // ---------------------------------------------------------------------------
@@ -481,9 +487,9 @@ extern "C" int xk_causal_conv1d_update(
                     stride_o_batch == dim && stride_state_line % 8 == 0 &&
                     aligned(x, 16) && aligned(out, 16) && aligned(conv_state, 16);
   if (fast) {
-    const dim3 grid(cdiv(dim, 256 * 8), batch);
+    const dim3 grid(cdiv(dim, kW4Block * 8), batch);
 #define XK_W4(T, WT)                                                            \
-  hipLaunchKernelGGL((conv1d_update_w4_kernel<T, WT>), grid, dim3(256), 0, s,   \
+  hipLaunchKernelGGL((conv1d_update_w4_kernel<T, WT>), grid, dim3(kW4Block), 0, s, \
                      static_cast<const T*>(x), static_cast<T*>(out),            \
                      static_cast<T*>(conv_state), stride_state_line,            \
                      static_cast<const WT*>(weight), wdtype, bias,              \

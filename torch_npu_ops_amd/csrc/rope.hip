@@ -55,11 +55,18 @@ __device__ __forceinline__ void ld_f32(const T* p, float (&o)[N]) {
 }
 
 template <typename T, int N>
+__device__ __forceinline__ void vec_f32(const Vec<T, N>& v, float (&o)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) o[i] = to_f32(v.v[i]);
+}
+
+// Non-temporal store of N floats converted to T (outputs are written once).
+template <typename T, int N>
 __device__ __forceinline__ void st_f32(T* p, const float (&in)[N]) {
   Vec<T, N> v;
 #pragma unroll
   for (int i = 0; i < N; ++i) v.v[i] = from_f32<T>(in[i]);
-  *reinterpret_cast<Vec<T, N>*>(p) = v;
+  st_stream(reinterpret_cast<Vec<T, N>*>(p), v);
 }
 
 template <typename T, typename A, int HD>
@@ -80,14 +87,16 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
   const int d0 = lane * kVec;
 
   const T* row = reinterpret_cast<const T*>(p.qkv) + tok * p.stride_row;
+  using VT = Vec<T, kVec>;
+  using VA = Vec<A, kVec>;
   if (h >= p.hq + p.hkv) {  // v: copy through
     const int hv = h - p.hq - p.hkv;
     const T* src = row + p.q_hidden + p.kv_hidden + static_cast<int64_t>(hv) * HD;
     T* dst = reinterpret_cast<T*>(p.v) + tok * p.kv_hidden + static_cast<int64_t>(hv) * HD;
-    using VT = Vec<T, kVec>;
-    *reinterpret_cast<VT*>(dst + d0) = *reinterpret_cast<const VT*>(src + d0);
-    *reinterpret_cast<VT*>(dst + kHalf + d0) =
-        *reinterpret_cast<const VT*>(src + kHalf + d0);
+    const VT a = ld_stream(reinterpret_cast<const VT*>(src + d0));
+    const VT c = ld_stream(reinterpret_cast<const VT*>(src + kHalf + d0));
+    st_stream(reinterpret_cast<VT*>(dst + d0), a);
+    st_stream(reinterpret_cast<VT*>(dst + kHalf + d0), c);
     return;
   }
   const bool is_q = h < p.hq;
@@ -98,33 +107,43 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
   const A* w = reinterpret_cast<const A*>(is_q ? p.qw : p.kw);
   const A* b = reinterpret_cast<const A*>(is_q ? p.qb : p.kb);
 
+  // Every load of the item is issued before the first use, so the kernel
+  // pays one memory latency: x (streamed), then weights, bias and sin/cos
+  // (shared by many items, served from cache).
+  const VT xa = ld_stream(reinterpret_cast<const VT*>(src + d0));
+  const VT xb = ld_stream(reinterpret_cast<const VT*>(src + kHalf + d0));
+  const VA wa = *reinterpret_cast<const VA*>(w + d0);
+  const VA wb = *reinterpret_cast<const VA*>(w + kHalf + d0);
+  // Without a bias the bias loads read the weight (valid memory) and are
+  // multiplied by zero, so no branch separates the loads.
+  const float b_scale = b ? 1.f : 0.f;
+  const A* bsrc = b ? b : w;
+  const VA ba = *reinterpret_cast<const VA*>(bsrc + d0);
+  const VA bb = *reinterpret_cast<const VA*>(bsrc + kHalf + d0);
+  VA ca, cb, sa, sb;
+  if (!p.pos) {
+    const A* cs = reinterpret_cast<const A*>(p.cos) + tok * p.stride_sc;
+    const A* sn = reinterpret_cast<const A*>(p.sin) + tok * p.stride_sc;
+    ca = *reinterpret_cast<const VA*>(cs + d0);
+    cb = *reinterpret_cast<const VA*>(cs + kHalf + d0);
+    sa = *reinterpret_cast<const VA*>(sn + d0);
+    sb = *reinterpret_cast<const VA*>(sn + kHalf + d0);
+  }
+
   float x1[kVec], x2[kVec];
-  ld_f32<T, kVec>(src + d0, x1);
-  ld_f32<T, kVec>(src + kHalf + d0, x2);
+  vec_f32(xa, x1);
+  vec_f32(xb, x2);
   float ss = 0.f;
 #pragma unroll
   for (int u = 0; u < kVec; ++u) ss = fmaf(x1[u], x1[u], fmaf(x2[u], x2[u], ss));
   ss = group_sum<kTeam>(ss);
   const float r = 1.0f / sqrtf(ss * (1.0f / HD) + p.eps);
 
-  float w1[kVec], w2[kVec];
-  ld_f32<A, kVec>(w + d0, w1);
-  ld_f32<A, kVec>(w + kHalf + d0, w2);
   float n1[kVec], n2[kVec];
 #pragma unroll
   for (int u = 0; u < kVec; ++u) {
-    n1[u] = x1[u] * r * w1[u];
-    n2[u] = x2[u] * r * w2[u];
-  }
-  if (b) {
-    float b1[kVec], b2[kVec];
-    ld_f32<A, kVec>(b + d0, b1);
-    ld_f32<A, kVec>(b + kHalf + d0, b2);
-#pragma unroll
-    for (int u = 0; u < kVec; ++u) {
-      n1[u] += b1[u];
-      n2[u] += b2[u];
-    }
+    n1[u] = fmaf(x1[u] * r, to_f32(wa.v[u]), to_f32(ba.v[u]) * b_scale);
+    n2[u] = fmaf(x2[u] * r, to_f32(wb.v[u]), to_f32(bb.v[u]) * b_scale);
   }
 
   float c1[kVec], c2[kVec], s1[kVec], s2[kVec];
@@ -141,12 +160,10 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
       c2[u] = c1[u];
     }
   } else {
-    const A* cs = reinterpret_cast<const A*>(p.cos) + tok * p.stride_sc;
-    const A* sn = reinterpret_cast<const A*>(p.sin) + tok * p.stride_sc;
-    ld_f32<A, kVec>(cs + d0, c1);
-    ld_f32<A, kVec>(cs + kHalf + d0, c2);
-    ld_f32<A, kVec>(sn + d0, s1);
-    ld_f32<A, kVec>(sn + kHalf + d0, s2);
+    vec_f32(ca, c1);
+    vec_f32(cb, c2);
+    vec_f32(sa, s1);
+    vec_f32(sb, s2);
   }
   float o1[kVec], o2[kVec];
 #pragma unroll
