@@ -72,6 +72,7 @@ struct ChunkParams {
   int cu_i64;
   int32_t* chunk_off;  // [N+1] workspace
   int32_t* seq_order;  // [N] workspace: sequences, longest first
+  int2* ctab;          // [NTmax] workspace: (first token, length) per chunk
   bf16* dump;          // [64 * 32] workspace: sink for padded-row stores
   char* rec;           // [NTmax, HV] records of kRec bytes, workspace
   int64_t N, NTmax;
@@ -93,6 +94,35 @@ __device__ __forceinline__ char* rec_at(const ChunkParams& p, int64_t c, int hv)
 // P1: one wave per (chunk, v-head); waves of a block are independent.
 // ---------------------------------------------------------------------------
 
+// r[row] = 1 / sqrt(sum x^2 + 1e-6) for the 64 rows of a chunk held as MFMA
+// A operands (lane: row mi*16 + l15, elements kk*32 + 8*lg ...), or 1 when
+// `on` is 0.  Sums use bf16 dot2 (exact products, fp32 accumulation).
+template <int KK>
+__device__ __forceinline__ void row_scales(const bf8_t (&x)[4][KK], float* r, int on) {
+  const int lane = threadIdx.x & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  if (!on) {
+    if (lg == 0)
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) r[mi * 16 + l15] = 1.0f;
+    return;
+  }
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) {
+    float ss = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const bf2_t pr = {x[mi][kk][e], x[mi][kk][e + 1]};
+        ss = __builtin_amdgcn_fdot2_f32_bf16(pr, pr, ss, false);
+      }
+    ss += __shfl_xor(ss, 16, kWave);
+    ss += __shfl_xor(ss, 32, kWave);
+    if (lg == 0) r[mi * 16 + l15] = 1.0f / sqrtf(ss + 1e-6f);
+  }
+}
+
 template <int K, typename GT, typename BT>
 __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   __shared__ __align__(16) float lds[4][kC][kLd];
@@ -102,10 +132,11 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   const int l15 = lane & 15, lg = lane >> 4;
   const int64_t c = blockIdx.x;
   const int hv = blockIdx.y * 4 + wid;
-  int64_t n, s;
-  int L;
+  const int2 ce = p.ctab[c];  // (first token, length); length 0 past the last chunk
+  const int64_t s = ce.x;
+  const int L = ce.y;
   // Wave-uniform exit; the kernel has no block-level barriers.
-  if (!(hv < p.HV && locate_chunk(p, c, n, s, L))) return;
+  if (!(hv < p.HV && L > 0)) return;
   float (*X)[kLd] = lds[wid];
   float* gcv = vec[wid][0];
   float* btv = vec[wid][1];
@@ -115,13 +146,19 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   constexpr int KK = K / 32;
   const int64_t rs = static_cast<int64_t>(p.H) * K;
 
-  // K rows of the chunk as MFMA operands (A and B^T read the same rows).
-  bf8_t kop[4][KK];
+  // K rows of the chunk as MFMA operands (A and B^T read the same rows),
+  // and the Q rows, all issued up front so the wave pays one load latency.
+  bf8_t kop[4][KK], qop[4][KK];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
       kop[mi][kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      qop[mi][kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
   // Per-token g (inclusive scan within the chunk) and beta; padded rows 0
   // (loads clamped to row L-1, then selected away).
   const int lt = min(lane, L - 1);
@@ -137,21 +174,10 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   gcv[lane] = gv;
   btv[lane] = bv;
   // Row scales r = 1 / sqrt(sum x^2 + 1e-6) of the rows this lane holds
-  // (row mi*16 + l15; the four lg lanes hold its four 32-wide pieces).
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    float ss = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = static_cast<float>(kop[mi][kk][e]);
-        ss = fmaf(x, x, ss);
-      }
-    ss += __shfl_xor(ss, 16, kWave);
-    ss += __shfl_xor(ss, 32, kWave);
-    if (lg == 0) rkv[mi * 16 + l15] = p.l2norm ? 1.0f / sqrtf(ss + 1e-6f) : 1.0f;
-  }
+  // (row mi*16 + l15; the four lg lanes hold its four 32-wide pieces), or 1
+  // without the in-op l2norm.
+  row_scales<KK>(kop, rkv, p.l2norm);
+  row_scales<KK>(qop, rqv, p.l2norm);
   __builtin_amdgcn_wave_barrier();
 
   // M = strict_tril(b_i r_i r_j (k_i . k_j) exp(gc_i - gc_j)) into X (the
@@ -192,27 +218,6 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   __builtin_amdgcn_wave_barrier();
 
   // Aq = scale * tril(r_q r_k (q k^T) exp(gc_i - gc_j)), rows < L.
-  bf8_t qop[4][KK];
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qop[mi][kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    float ss = 0.f;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float y = static_cast<float>(qop[mi][kk][e]);
-        ss = fmaf(y, y, ss);
-      }
-    ss += __shfl_xor(ss, 16, kWave);
-    ss += __shfl_xor(ss, 32, kWave);
-    if (lg == 0) rqv[mi * 16 + l15] = p.l2norm ? 1.0f / sqrtf(ss + 1e-6f) : 1.0f;
-  }
-  __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -420,8 +425,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 #pragma unroll
       for (int nj = 0; nj < 2; ++nj) {
         Vec<__bf16, 4> h, l;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) split(sreg[m2][nj][i], h.v[i], l.v[i]);
+        split4(sreg[m2][nj], h, l);
         const int k0 = wid * (K / 4) + m2 * 16 + 4 * lg;
         *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][nj * 16 + l15][k0]) = h;
         *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[1][nj * 16 + l15][k0]) = l;
@@ -472,11 +476,10 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj) {
       Vec<__bf16, 4> h, l;
+      f4_t rv;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float rv = cur.bt[i] * to_f32(cur.v[nj][i]) - cur.ck[i] * ks[nj][i];
-        split(rv, h.v[i], l.v[i]);
-      }
+      for (int i = 0; i < 4; ++i) rv[i] = cur.bt[i] * to_f32(cur.v[nj][i]) - cur.ck[i] * ks[nj][i];
+      split4(rv, h, l);
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = h;
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = l;
     }
@@ -498,11 +501,13 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj) {
       Vec<__bf16, 4> b, h, l;
+      f4_t d;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         b.v[i] = static_cast<__bf16>(vn[nj][i]);
-        split(inv.ed[i] * vn[nj][i], h.v[i], l.v[i]);
+        d[i] = inv.ed[i] * vn[nj][i];
       }
+      split4(d, h, l);
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.vt[nj * 16 + l15][wid * 16 + 4 * lg]) = b;
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = h;
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = l;
@@ -595,7 +600,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 template <int K, typename GT, typename BT>
 int launch_chunk(const ChunkParams& p, int64_t V, hipStream_t s) {
   hipLaunchKernelGGL(chunk_offsets_kernel<ChunkParams>, dim3(1), dim3(256), 0, s, p,
-                     p.seq_order);
+                     p.seq_order, p.ctab, p.NTmax);
   int st = launch_status();
   if (st) return st;
   hipLaunchKernelGGL((gdn_chunk_prep_kernel<K, GT, BT>), dim3(p.NTmax, (p.HV + 3) / 4),
@@ -628,8 +633,9 @@ using namespace xk;
 extern "C" int64_t xk_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t num_seqs,
                                                 int64_t HV) {
   if (total_tokens < 0 || num_seqs < 0 || HV <= 0) return -1;
-  return align256(4 * (num_seqs + 1)) + align256(4 * num_seqs) + kDump +
-         nt_max(total_tokens, num_seqs) * HV * kRec;
+  const int64_t nt = nt_max(total_tokens, num_seqs);
+  return align256(4 * (num_seqs + 1)) + align256(4 * num_seqs) + align256(8 * nt) + kDump +
+         nt * HV * kRec;
 }
 
 extern "C" int xk_gdn_chunk_fwd(
@@ -648,6 +654,8 @@ extern "C" int xk_gdn_chunk_fwd(
   if (cu_dtype != XK_I32 && cu_dtype != XK_I64) return XK_ERR_UNSUPPORTED;
   if (K != 128 || V % kBV != 0 || V <= 0) return XK_ERR_UNSUPPORTED;
   if (N == 0 || total_tokens == 0) return XK_OK;
+  // Token indices travel as int32 in the chunk table.
+  if (total_tokens > INT32_MAX - kC) return XK_ERR_UNSUPPORTED;
   if (!q || !k || !v || !g || !beta || !o || !cu_seqlens) return XK_ERR_INVALID;
   if (!aligned(q, 16) || !aligned(k, 16)) return XK_ERR_INVALID;
   const int64_t need = xk_gdn_chunk_workspace_bytes(total_tokens, N, HV);
@@ -669,6 +677,8 @@ extern "C" int xk_gdn_chunk_fwd(
   ws += align256(4 * (N + 1));
   p.seq_order = reinterpret_cast<int32_t*>(ws);
   ws += align256(4 * N);
+  p.ctab = reinterpret_cast<int2*>(ws);
+  ws += align256(8 * nt_max(total_tokens, N));
   p.dump = reinterpret_cast<bf16*>(ws);
   p.rec = ws + kDump;
   p.N = N;

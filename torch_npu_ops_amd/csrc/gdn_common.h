@@ -30,19 +30,53 @@ __device__ __forceinline__ void split(float x, __bf16& hi, __bf16& lo) {
   lo = static_cast<__bf16>(x - static_cast<float>(hi));
 }
 
+typedef float f2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+
+// split() of two values at once, with the same results: one packed
+// conversion rounds both hi values, a shift and a mask widen them back to
+// fp32, and a second packed conversion rounds both remainders (about half
+// the instructions of two scalar splits, and the outputs come out packed).
+__device__ __forceinline__ void split2(float a, float b, bf2_t& hi, bf2_t& lo) {
+  hi = __builtin_convertvector(f2_t{a, b}, bf2_t);
+  const uint32_t u = __builtin_bit_cast(uint32_t, hi);
+  const float ha = __builtin_bit_cast(float, u << 16);
+  const float hb = __builtin_bit_cast(float, u & 0xffff0000u);
+  lo = __builtin_convertvector(f2_t{a - ha, b - hb}, bf2_t);
+}
+
+// Four values (an MFMA C fragment) split into hi / lo bf16 quads.
+__device__ __forceinline__ void split4(const f4_t& x, Vec<__bf16, 4>& h, Vec<__bf16, 4>& l) {
+  bf2_t h0, l0, h1, l1;
+  split2(x[0], x[1], h0, l0);
+  split2(x[2], x[3], h1, l1);
+  h.v[0] = h0[0];
+  h.v[1] = h0[1];
+  h.v[2] = h1[0];
+  h.v[3] = h1[1];
+  l.v[0] = l0[0];
+  l.v[1] = l0[1];
+  l.v[2] = l1[0];
+  l.v[3] = l1[1];
+}
+
 // Eight consecutive fp32 values (16-byte aligned) split into hi / lo.
 __device__ __forceinline__ void split8(const float* p, bf8_t& h, bf8_t& l) {
   const f4_t a = *reinterpret_cast<const f4_t*>(p);
   const f4_t b = *reinterpret_cast<const f4_t*>(p + 4);
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    __bf16 x, y;
-    split(a[e], x, y);
-    h[e] = x;
-    l[e] = y;
-    split(b[e], x, y);
-    h[e + 4] = x;
-    l[e + 4] = y;
+  for (int e = 0; e < 4; e += 2) {
+    bf2_t x, y;
+    split2(a[e], a[e + 1], x, y);
+    h[e] = x[0];
+    h[e + 1] = x[1];
+    l[e] = y[0];
+    l[e + 1] = y[1];
+    split2(b[e], b[e + 1], x, y);
+    h[e + 4] = x[0];
+    h[e + 5] = x[1];
+    l[e + 4] = y[0];
+    l[e + 5] = y[1];
   }
 }
 
@@ -92,9 +126,12 @@ constexpr int64_t kSortMaxSeqs = 2048;
 // chunk_off[n] = sum_{m<n} ceil(len_m / 64), chunk_off[N] = total chunks.
 // If `order` is given, order[r] = the sequence of rank r when sequences are
 // sorted by chunk count, longest first (ties by index), or order[r] = r for
-// more than kSortMaxSeqs sequences.  One block of 256 threads.
+// more than kSortMaxSeqs sequences.  If `table` is given (ntab entries),
+// table[c] = (first token, length) of global chunk c, (0, 0) past the last
+// chunk; token indices must fit in int32.  One block of 256 threads.
 template <class P>
-__global__ void __launch_bounds__(256) chunk_offsets_kernel(P p, int32_t* order) {
+__global__ void __launch_bounds__(256) chunk_offsets_kernel(P p, int32_t* order, int2* table,
+                                                            int64_t ntab) {
   constexpr int kT = 256;
   __shared__ int32_t part[kT];
   const int tid = threadIdx.x;
@@ -119,6 +156,24 @@ __global__ void __launch_bounds__(256) chunk_offsets_kernel(P p, int32_t* order)
     acc += seq_chunks(p, n);
   }
   if (tid == kT - 1) p.chunk_off[p.N] = acc;
+  if (table) {
+    __syncthreads();  // chunk_off complete and visible to the block
+    const int64_t total = p.chunk_off[p.N];
+    for (int64_t c = tid; c < ntab; c += kT) {
+      int2 e = make_int2(0, 0);
+      if (c < total) {
+        int64_t lo = 0, hi = p.N;  // chunk_off[lo] <= c < chunk_off[hi]
+        while (hi - lo > 1) {
+          const int64_t mid = (lo + hi) >> 1;
+          if (p.chunk_off[mid] <= c) lo = mid; else hi = mid;
+        }
+        const int64_t s0 = cu_at(p, lo) + (c - p.chunk_off[lo]) * kC;
+        e = make_int2(static_cast<int>(s0),
+                      static_cast<int>(min<int64_t>(kC, cu_at(p, lo + 1) - s0)));
+      }
+      table[c] = e;
+    }
+  }
   if (!order) return;
   // Ranks are a permutation of [0, N): distinct (chunks, index) keys.
   const bool sort = p.N <= kSortMaxSeqs;

@@ -569,7 +569,8 @@ int seq_init(Seq& q, const void* cu, xk_dtype cu_dtype, int64_t N, int64_t T, vo
 
 template <class P>
 int launch_offsets(const P& p, hipStream_t s) {
-  hipLaunchKernelGGL(chunk_offsets_kernel<P>, dim3(1), dim3(256), 0, s, p, nullptr);
+  hipLaunchKernelGGL(chunk_offsets_kernel<P>, dim3(1), dim3(256), 0, s, p, nullptr, nullptr,
+                     int64_t{0});
   return launch_status();
 }
 
