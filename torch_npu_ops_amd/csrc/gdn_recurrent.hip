@@ -255,6 +255,25 @@ __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
   auto slot_of = [&](int64_t col) -> int64_t {
     return p.idx ? p.idx[n * p.idx_s0 + col * p.idx_s1] : n;
   };
+  // One token's inputs: lane tid holds element tid of q, k (tid < K) and v
+  // (tid < V), plus the head's g and beta.
+  const int tid = threadIdx.x;
+  struct TokIn {
+    float q, k, v, g, b;
+  };
+  auto load_in = [&](int64_t tok) {
+    TokIn r;
+    r.q = tid < K ? ldf<T>(p.q, (tok * p.H + hq) * K + tid) : 0.f;
+    r.k = tid < K ? ldf<T>(p.k, (tok * p.H + hq) * K + tid) : 0.f;
+    r.v = tid < V ? ldf<T>(p.v, (tok * p.HV + hv) * V + tid) : 0.f;
+    r.g = ldf<GT>(p.g, tok * p.HV + hv);
+    r.b = p.beta ? ldf<BT>(p.beta, tok * p.HV + hv) : 1.0f;
+    return r;
+  };
+  // The first token's inputs are fetched before the state tile: loads
+  // complete in issue order, so the q/k normalisation then overlaps the
+  // tile's latency instead of waiting behind it.
+  TokIn cur = load_in(bos);
   Tile<K, V> t;
   const int64_t s0 = slot_of(first_col);
   const bool s0_ok = p.h0 && s0 >= 0 && s0 < p.slots && first_col >= 0;
@@ -268,13 +287,13 @@ __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
   const bool per_token = p.inplace && p.idx && p.idx_s1 != 0;
   for (int64_t i = 0; i < len; ++i) {
     const int64_t tok = bos + i;
-    prep_qk<K, V>(sm, [&](int which, int e) {
-      const void* src = which == 0 ? p.q : p.k;
-      return ldf<T>(src, (tok * p.H + hq) * K + e);
-    }, p.l2norm, p.scale);
-    if (threadIdx.x < V) sm.v[threadIdx.x] = ldf<T>(p.v, (tok * p.HV + hv) * V + threadIdx.x);
-    const float decay = __expf(ldf<GT>(p.g, tok * p.HV + hv));
-    const float beta = p.beta ? ldf<BT>(p.beta, tok * p.HV + hv) : 1.0f;
+    // The next token's inputs are fetched while this one computes.
+    const TokIn nxt = i + 1 < len ? load_in(tok + 1) : cur;
+    prep_qk<K, V>(sm, [&](int which, int) { return which == 0 ? cur.q : cur.k; },
+                  p.l2norm, p.scale);
+    if (tid < V) sm.v[tid] = cur.v;
+    const float decay = __expf(cur.g);
+    const float beta = cur.b;
     T* o = reinterpret_cast<T*>(p.o) + (tok * p.HV + hv) * V;
     gdn_token<K, V>(t, sm, decay, beta, [&](int c, float val) { o[c] = from_f32<T>(val); });
     if (per_token) {
@@ -282,6 +301,7 @@ __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
       if (sl >= 0 && sl < p.slots)
         store_tile<K, V>(t, p.ht + sl * p.ht_slot_stride + static_cast<int64_t>(hv) * K * V);
     }
+    cur = nxt;
   }
   if (!per_token) {
     if (p.inplace) {
