@@ -189,6 +189,7 @@ struct VarlenParams {
   int silu_on;
   int32_t pad;
   int w_vec;  // weights are [D, W] contiguous, x's dtype, 16-byte aligned
+  int64_t ncb, ntt;  // prefill grid: channel blocks x token tiles
 };
 
 __device__ __forceinline__ int64_t resolve_slot(const VarlenParams& p, int s,
@@ -236,14 +237,23 @@ constexpr bool kNtLoad = (XK_CONV_NT & 2) != 0;
 template <typename T, int W, int VEC, bool SILU>
 __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
   using VT = Vec<T, VEC>;
-  const int64_t c0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC;
+  // XCD-aware block order: block b runs on XCD b % 8, and the remapped index
+  // gives each XCD a contiguous run of (channel block, token tile) pairs,
+  // token tiles fastest.  A tile's halo (the last W-1 inputs of the previous
+  // tile) is then usually still in that XCD's L2.  The grid is 8 * per
+  // blocks, so the remap is a permutation of [0, 8 * per).
+  const int64_t nblk = p.ncb * p.ntt;
+  const int64_t per = (nblk + 7) / 8;
+  const int64_t bid = static_cast<int64_t>(blockIdx.x & 7) * per + (blockIdx.x >> 3);
+  if (bid >= nblk) return;
+  const int64_t tile = bid % p.ntt;
+  const int64_t cb = bid / p.ntt;
+  const int64_t c0 = (cb * 256 + threadIdx.x) * VEC;
   if (c0 >= p.D) return;
   // Tokens outside [qsl[0], qsl[B]) belong to no sequence and are skipped.
-  const int64_t t0 = max(static_cast<int64_t>(blockIdx.y) * kTileT,
-                         static_cast<int64_t>(p.qsl[0]));
+  const int64_t t0 = max(tile * kTileT, static_cast<int64_t>(p.qsl[0]));
   const int64_t total = p.qsl[p.B];
-  const int64_t t_end = min(min(static_cast<int64_t>(blockIdx.y + 1) * kTileT, total),
-                            p.num_tokens);
+  const int64_t t_end = min(min((tile + 1) * kTileT, total), p.num_tokens);
   if (t0 >= t_end) return;
 
   float wt[W][VEC], bs[VEC];
@@ -423,8 +433,12 @@ __global__ void __launch_bounds__(256) conv1d_varlen_state_kernel(VarlenParams p
 }
 
 template <typename T, int VEC>
-int launch_varlen_w(const VarlenParams& p, hipStream_t s) {
-  const dim3 grid(cdiv(p.D, 256 * VEC), cdiv(p.num_tokens, kTileT));
+int launch_varlen_w(VarlenParams p, hipStream_t s) {
+  p.ncb = cdiv(p.D, 256 * VEC);
+  p.ntt = cdiv(p.num_tokens, kTileT);
+  const int64_t per = cdiv(p.ncb * p.ntt, 8);
+  if (8 * per > INT32_MAX) return XK_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<uint32_t>(8 * per));
   switch (p.W) {
 #define XK_W(n) \
   case n:                                                                       \
