@@ -437,6 +437,108 @@ class GdnRecurrentCase(Case):
         return run, f"{n} of 256 sequences, fp32", a.B / n
 
 
+class GdnGatingCase(Case):
+    name = "gdn_gating"
+    config = ("next row (npu_fused_gdn_gating) on the prefill shape: 16384 tokens x 32 "
+              "v heads, bf16 a/b ~N(0,1), fp32 A_log ~N(0,1) and dt_bias ~N(0,1); "
+              "outputs fp32 g and bf16 beta")
+    kernel = "gdn_gating_kernel"
+    timing = "graph"
+    R, HV = 16384, 32
+    # a, b (bf16) + g (fp32) + beta (bf16) + A_log / dt_bias
+    algo_bytes = R * HV * (2 + 2 + 4 + 2) + HV * 8
+
+    def __init__(self):
+        g = torch.Generator().manual_seed(0)
+        self.A_log = torch.randn(self.HV, generator=g)
+        self.dt_bias = torch.randn(self.HV, generator=g)
+        self.a = _randn((self.R, self.HV), g, torch.bfloat16)
+        self.b = _randn((self.R, self.HV), g, torch.bfloat16)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        A_log, dt_bias = self.A_log.to(dev), self.dt_bias.to(dev)
+        out = []
+        for _ in range(n):
+            a, b = self.a.to(dev), self.b.to(dev)
+            gg = torch.empty(self.R, self.HV, device=dev)
+            bo = torch.empty_like(b)
+
+            def run(a=a, b=b, gg=gg, bo=bo):
+                _ok(lib.xk_fused_gdn_gating(A_log.data_ptr(), a.data_ptr(), b.data_ptr(),
+                                            dt_bias.data_ptr(), gg.data_ptr(), bo.data_ptr(),
+                                            self.R, self.HV, 1.0, 20.0, _lib.XK_BF16,
+                                            _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import gating as ogt
+        a = (self.A_log, self.a, self.b, self.dt_bias)
+        return (lambda: ogt.fused_gdn_gating(*a),
+                "full shape (16384 x 32), fp32", 1.0)
+
+
+class GdnSigmoidGatingCase(Case):
+    name = "gdn_sigmoid_gating_update"
+    config = ("next row (npu_fused_sigmoid_gating_delta_rule_update) on config 5's "
+              "decode shapes: 256 sequences x 1 token, 16 qk / 32 v heads, head_dim 128, "
+              "fp32 state [256,32,128,128] in place, in-kernel gating from bf16 a/b "
+              "and l2norm")
+    kernel = "gdn_recurrent_kernel"
+    I = GdnDecodeInputs
+    # state r/w + q/k/v + a/b + o
+    algo_bytes = (I.B * I.HV * I.K * I.V * 4 * 2 + I.B * (2 * I.H * I.K + I.HV * I.V) * 2
+                  + I.B * I.HV * 2 * 2 + I.B * I.HV * I.V * 2 + I.HV * 8)
+
+    def __init__(self):
+        a = self.inp = GdnDecodeInputs()
+        g = torch.Generator().manual_seed(1)
+        self.q = a.x[:, :a.H * a.K].reshape(a.B, 1, a.H, a.K).contiguous()
+        self.k = a.x[:, a.H * a.K:2 * a.H * a.K].reshape(a.B, 1, a.H, a.K).contiguous()
+        self.v = a.x[:, 2 * a.H * a.K:].reshape(a.B, 1, a.HV, a.V).contiguous()
+        self.ga = _randn((a.B, 1, a.HV), g, torch.bfloat16)
+        self.gb = _randn((a.B, 1, a.HV), g, torch.bfloat16)
+        self.A_log = torch.randn(a.HV, generator=g)
+        self.dt_bias = torch.randn(a.HV, generator=g)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        a = self.inp
+        q, k, v = self.q.to(dev), self.k.to(dev), self.v.to(dev)
+        ga, gb = self.ga.to(dev), self.gb.to(dev)
+        A_log, dt_bias, idx = self.A_log.to(dev), self.dt_bias.to(dev), a.idx.to(dev)
+        cu = torch.arange(a.B + 1, dtype=torch.int32, device=dev)
+        out = []
+        for _ in range(n):
+            st = a.state.to(dev)
+            o = torch.empty(a.B, 1, a.HV, a.V, dtype=torch.bfloat16, device=dev)
+
+            def run(st=st, o=o):
+                _ok(lib.xk_gdn_sigmoid_gating_update(
+                    A_log.data_ptr(), ga.data_ptr(), dt_bias.data_ptr(), 1.0, 20.0,
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), gb.data_ptr(), _lib.XK_BF16,
+                    o.data_ptr(), st.data_ptr(), st.stride(0), a.B, idx.data_ptr(),
+                    cu.data_ptr(), a.B, a.H, a.HV, a.K, a.V, a.K ** -0.5, 1, _lib.XK_BF16,
+                    _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import gating as ogt
+        a = self.inp
+        n = 16
+
+        def run():
+            ogt.sigmoid_gating_delta_rule_update(
+                self.A_log, self.ga[:n], self.dt_bias, self.q[:n], self.k[:n], self.v[:n],
+                self.gb[:n], a.state[:n], a.idx[:n], torch.arange(n + 1, dtype=torch.int32),
+                a.K ** -0.5, True, dtype=torch.float32)
+        return run, f"{n} of 256 sequences, fp32", a.B / n
+
+
 def chunk_gdn_flops(tokens, HV, K=128, V=128, C=64):
     """Algorithmic FLOPs of the chunked gated delta rule per call, summed
     per 64-token chunk and v-head: K K^T, Q K^T (2C^2K each), W = A(k b e^g)
@@ -511,7 +613,7 @@ class GdnChunkCase(Case):
 
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
                              ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase,
-                             GdnChunkCase)}
+                             GdnChunkCase, GdnGatingCase, GdnSigmoidGatingCase)}
 HEADLINE = "layer_norm_fwd"
 
 

@@ -199,6 +199,48 @@ int xk_gdn_recurrent(
     int use_qk_l2norm, int inplace_final_state, void* stream);
 
 /* ------------------------------------------------------------------------
+ * GDN gating (the step before both gated-delta-rule forms).
+ * Replaces xllm::kernel::npu::npu_fused_gdn_gating
+ *   (triton_npu/torch_api/triton_ops_api.h:73-79,
+ *    npu_triton_fused_gdn_gating.cpp:33-94; kernel
+ *    triton_src/test_fused_gdn_gating.py:10-43).
+ *   For rows x heads (a, b [rows, heads] in ab_dtype; A_log, dt_bias fp32
+ *   [heads]):
+ *     x        = a + dt_bias
+ *     g        = -exp(A_log) * (softplus_beta * x <= threshold
+ *                               ? log(1 + exp(softplus_beta * x)) / softplus_beta
+ *                               : x)                        (fp32 [rows, heads])
+ *     beta_out = sigmoid(b)                                  (ab_dtype)
+ */
+int xk_fused_gdn_gating(const float* A_log, const void* a, const void* b,
+                        const float* dt_bias, float* g_out, void* beta_out,
+                        int64_t rows, int64_t heads, float softplus_beta,
+                        float threshold, xk_dtype ab_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Recurrent gated delta rule with the gating computed in the kernel.
+ * Replaces xllm::kernel::npu::npu_fused_sigmoid_gating_delta_rule_update
+ *   (triton_npu/torch_api/triton_ops_api.h:95-109,
+ *    npu_triton_fused_sigmoid_gating_delta_rule_update.cpp:54-177; kernel
+ *    triton_src/test_fused_sigmoid_gating_delta_rule_update.py:10-117).
+ *   Per token, g and beta come from a and b ([tokens, HV], ab_dtype) as in
+ *   xk_fused_gdn_gating; then the recurrent step of xk_gdn_recurrent runs.
+ *   Sequences are cu_seqlens[n]..cu_seqlens[n+1] (int32).  The state pool
+ *   state [num_slots, HV, K, V] (fp32) is updated in place: sequence n
+ *   starts from state[state_indices[n]] and writes its final state there; a
+ *   negative (or out-of-range) index starts from zeros and writes nothing.
+ *   o : [tokens, HV, V] in dtype.  use_qk_l2norm normalises q and k by
+ *   1/sqrt(sum^2 + 1e-6) before `scale`.  (K, V) in {64, 128}^2.
+ */
+int xk_gdn_sigmoid_gating_update(
+    const float* A_log, const void* a, const float* dt_bias, float softplus_beta,
+    float threshold, const void* q, const void* k, const void* v, const void* b,
+    xk_dtype ab_dtype, void* o, float* state, int64_t stride_state_slot,
+    int64_t num_slots, const int32_t* state_indices, const int32_t* cu_seqlens,
+    int64_t N, int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+    int use_qk_l2norm, xk_dtype dtype, void* stream);
+
+/* ------------------------------------------------------------------------
  * a8. One decode step of the gated delta rule fused with the causal conv1d
  * update of its mixed q/k/v projection (no single reference function: the
  * composition of npu_causal_conv1d_update, the [q | k | v] channel split of

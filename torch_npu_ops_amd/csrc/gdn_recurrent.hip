@@ -61,6 +61,20 @@ __device__ __forceinline__ float ldf(const void* p, int64_t i) {
   return to_f32(reinterpret_cast<const T*>(p)[i]);
 }
 
+// GDN gating (triton_src/test_fused_gdn_gating.py:30-43): the log-decay
+// g = -exp(A_log) * softplus_{beta, threshold}(a + dt_bias), where softplus
+// is log(1 + exp(beta x)) / beta below the threshold and x above it.
+__device__ __forceinline__ float gdn_log_decay(float a_plus_bias, float A_log, float sp_beta,
+                                               float threshold) {
+  const float bx = sp_beta * a_plus_bias;
+  const float sp = bx <= threshold ? log1pf(expf(bx)) / sp_beta : a_plus_bias;
+  return -expf(A_log) * sp;
+}
+
+// sigmoid with IEEE division and the accurate exp, so that a rounded
+// 16-bit result matches a CPU computation of the same expression.
+__device__ __forceinline__ float sigmoid_exact(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 // One token of the recurrence on the register tile.  Inputs (q, k already
 // normalised and q scaled) are in sm.q / sm.k / sm.v.  Writes o[V] through
 // `out` (fp32 values, converted by the caller's store functor).
@@ -229,6 +243,12 @@ struct RecParams {
   float scale;
   int l2norm;
   int inplace;
+  // Gating mode: g holds a and beta holds b ([tokens, HV]); per token
+  // g = gdn_log_decay(a + dt_bias, A_log), beta = sigmoid(b).
+  int gating;
+  const float* A_log;
+  const float* dt_bias;
+  float sp_beta, sp_thr;
 };
 
 template <int K, int V, typename T, typename GT, typename BT>
@@ -268,6 +288,10 @@ __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
     r.v = tid < V ? ldf<T>(p.v, (tok * p.HV + hv) * V + tid) : 0.f;
     r.g = ldf<GT>(p.g, tok * p.HV + hv);
     r.b = p.beta ? ldf<BT>(p.beta, tok * p.HV + hv) : 1.0f;
+    if (p.gating) {
+      r.g = gdn_log_decay(r.g + p.dt_bias[hv], p.A_log[hv], p.sp_beta, p.sp_thr);
+      r.b = sigmoid_exact(r.b);
+    }
     return r;
   };
   // The first token's inputs are fetched before the state tile: loads
@@ -343,6 +367,37 @@ int rec_t(const RecParams& p, xk_dtype dt, xk_dtype gdt, xk_dtype bdt, hipStream
     case XK_F32: return rec_g<K, V, float>(p, gdt, bdt, s);
     default: return XK_ERR_UNSUPPORTED;
   }
+}
+
+// ---------------------------------------------------------------------------
+// GDN gating, elementwise over [rows, heads]: VEC consecutive elements per
+// lane.  Each element costs four transcendentals, so one element per lane
+// (the most lanes in flight) measured fastest on MI355X: 5.1 us for 16384 x
+// 32 elements, against 7.1 us with 8-element vectors.
+// ---------------------------------------------------------------------------
+template <typename AB, int VEC>
+__global__ void __launch_bounds__(256)
+    gdn_gating_kernel(const float* __restrict__ A_log, const AB* __restrict__ a,
+                      const AB* __restrict__ b, const float* __restrict__ dt_bias,
+                      float* __restrict__ g, AB* __restrict__ beta_out, int64_t n,
+                      int heads, float sp_beta, float threshold) {
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC;
+  if (i0 >= n) return;
+  using VA = Vec<AB, VEC>;
+  using VG = Vec<float, VEC>;
+  const VA av = ld_stream(reinterpret_cast<const VA*>(a + i0));
+  const VA bv = ld_stream(reinterpret_cast<const VA*>(b + i0));
+  VG gv;
+  VA ov;
+  int h = static_cast<int>(i0 % heads);
+#pragma unroll
+  for (int u = 0; u < VEC; ++u) {
+    gv.v[u] = gdn_log_decay(to_f32(av.v[u]) + dt_bias[h], A_log[h], sp_beta, threshold);
+    ov.v[u] = from_f32<AB>(sigmoid_exact(to_f32(bv.v[u])));
+    h = h + 1 == heads ? 0 : h + 1;
+  }
+  st_stream(reinterpret_cast<VG*>(g + i0), gv);
+  st_stream(reinterpret_cast<VA*>(beta_out + i0), ov);
 }
 
 // ---------------------------------------------------------------------------
@@ -577,4 +632,80 @@ extern "C" int xk_gdn_conv_decode(
     case XK_F32: return fused_g<128, 128, float>(p, g_dtype, bdt, s);
     default: return XK_ERR_UNSUPPORTED;
   }
+}
+
+extern "C" int xk_fused_gdn_gating(const float* A_log, const void* a, const void* b,
+                                   const float* dt_bias, float* g_out, void* beta_out,
+                                   int64_t rows, int64_t heads, float softplus_beta,
+                                   float threshold, xk_dtype ab_dtype, void* stream) {
+  if (rows < 0 || heads <= 0 || heads > INT32_MAX || softplus_beta == 0.f) return XK_ERR_INVALID;
+  if (!is_float_dtype(ab_dtype)) return XK_ERR_UNSUPPORTED;
+  if (rows == 0) return XK_OK;
+  if (!A_log || !a || !b || !dt_bias || !g_out || !beta_out) return XK_ERR_INVALID;
+  const int64_t n = rows * heads;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int hh = static_cast<int>(heads);
+#define XK_GATE(T, VEC)                                                                     \
+  hipLaunchKernelGGL((gdn_gating_kernel<T, VEC>), dim3(cdiv(n, 256 * VEC)), dim3(256), 0, s, \
+                     A_log, static_cast<const T*>(a), static_cast<const T*>(b), dt_bias,    \
+                     g_out, static_cast<T*>(beta_out), n, hh, softplus_beta, threshold)
+  switch (ab_dtype) {
+    case XK_BF16: XK_GATE(bf16, 1); break;
+    case XK_F16: XK_GATE(f16, 1); break;
+    default: XK_GATE(float, 1); break;
+  }
+#undef XK_GATE
+  return launch_status();
+}
+
+extern "C" int xk_gdn_sigmoid_gating_update(
+    const float* A_log, const void* a, const float* dt_bias, float softplus_beta,
+    float threshold, const void* q, const void* k, const void* v, const void* b,
+    xk_dtype ab_dtype, void* o, float* state, int64_t stride_state_slot,
+    int64_t num_slots, const int32_t* state_indices, const int32_t* cu_seqlens,
+    int64_t N, int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+    int use_qk_l2norm, xk_dtype dtype, void* stream) {
+  if (N < 0 || H <= 0 || HV <= 0 || HV % H != 0 || softplus_beta == 0.f) return XK_ERR_INVALID;
+  if (!is_float_dtype(dtype) || !is_float_dtype(ab_dtype)) return XK_ERR_UNSUPPORTED;
+  if (N == 0) return XK_OK;
+  if (!A_log || !a || !dt_bias || !q || !k || !v || !b || !o || !state || !state_indices ||
+      !cu_seqlens)
+    return XK_ERR_INVALID;
+  if (!aligned(state, 16) || stride_state_slot % 4) return XK_ERR_INVALID;
+  RecParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.g = a;
+  p.beta = b;
+  p.o = o;
+  p.h0 = state;
+  p.ht = state;
+  p.h0_slot_stride = stride_state_slot;
+  p.ht_slot_stride = stride_state_slot;
+  p.slots = num_slots;
+  p.cu = cu_seqlens;
+  p.cu_i64 = 0;
+  p.idx = state_indices;
+  p.idx_s0 = 1;
+  p.idx_s1 = 0;
+  p.accepted = nullptr;
+  p.N = N;
+  p.T = 0;
+  p.H = static_cast<int>(H);
+  p.HV = static_cast<int>(HV);
+  p.scale = scale;
+  p.l2norm = use_qk_l2norm;
+  p.inplace = 1;
+  p.gating = 1;
+  p.A_log = A_log;
+  p.dt_bias = dt_bias;
+  p.sp_beta = softplus_beta;
+  p.sp_thr = threshold;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (K == 128 && V == 128) return rec_t<128, 128>(p, dtype, ab_dtype, ab_dtype, s);
+  if (K == 64 && V == 64) return rec_t<64, 64>(p, dtype, ab_dtype, ab_dtype, s);
+  if (K == 128 && V == 64) return rec_t<128, 64>(p, dtype, ab_dtype, ab_dtype, s);
+  if (K == 64 && V == 128) return rec_t<64, 128>(p, dtype, ab_dtype, ab_dtype, s);
+  return XK_ERR_UNSUPPORTED;
 }

@@ -45,6 +45,9 @@ class OperationFactory {
              "layer_norm_fwd_kernel_fast_rms_bf16_z_nobias")
   XK_FACTORY(layer_norm_fwd_fast_rms_bf16_z_nobias_nomask, LayerNormFwdFastRMSBF16ZNoBiasNoMaskOp,
              "layer_norm_fwd_kernel_fast_rms_bf16_z_nobias_nomask")
+  XK_FACTORY(fused_gdn_gating, FusedGdnGatingOp, "fused_gdn_gating_decode_kernel")
+  XK_FACTORY(fused_sigmoid_gating_delta_rule_update, FusedSigmoidGatingDeltaRuleUpdateOp,
+             "fused_sigmoid_gating_delta_rule_update_kernel")
   XK_FACTORY(recurrent_gated_delta_rule_fwd, RecurrentGatedDeltaRuleFwdOp,
              "fused_recurrent_gated_delta_rule_fwd_kernel")
   XK_FACTORY(recurrent_gated_delta_rule_spec_fwd, RecurrentGatedDeltaRuleSpecFwdOp,

@@ -57,7 +57,9 @@ XK_OPERATION(LayerNormFwdFastBF16ZOp, xk_layer_norm_fwd);
 XK_OPERATION(LayerNormFwdFastRMSBF16ZBiasOp, xk_layer_norm_fwd);
 XK_OPERATION(LayerNormFwdFastRMSBF16ZNoBiasOp, xk_layer_norm_fwd);
 XK_OPERATION(LayerNormFwdFastRMSBF16ZNoBiasNoMaskOp, xk_layer_norm_fwd);
+XK_OPERATION(FusedGdnGatingOp, xk_fused_gdn_gating);
 XK_OPERATION(RecurrentGatedDeltaRuleFwdOp, xk_gdn_recurrent);
+XK_OPERATION(FusedSigmoidGatingDeltaRuleUpdateOp, xk_gdn_sigmoid_gating_update);
 XK_OPERATION(RecurrentGatedDeltaRuleSpecFwdOp, xk_gdn_recurrent);
 XK_OPERATION(ChunkGatedDeltaRuleFwdHOp, xk_chunk_fwd_h);
 XK_OPERATION(ChunkLocalCumsumScalarOp, xk_chunk_local_cumsum);

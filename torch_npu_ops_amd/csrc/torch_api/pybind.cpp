@@ -35,6 +35,13 @@ PYBIND11_MODULE(_xk_torch, m) {
         "initial_state"_a = OptT(), "inplace_final_state"_a = true, "cu_seqlens"_a = OptT(),
         "ssm_state_indices"_a = OptT(), "num_accepted_tokens"_a = OptT(),
         "use_qk_l2norm_in_kernel"_a = false);
+  m.def("npu_fused_gdn_gating", &npu::npu_fused_gdn_gating, "A_log"_a, "a"_a, "b"_a,
+        "dt_bias"_a, "beta"_a = 1.0f, "threshold"_a = 20.0f);
+  m.def("npu_fused_sigmoid_gating_delta_rule_update",
+        &npu::npu_fused_sigmoid_gating_delta_rule_update, "A_log"_a, "a"_a, "dt_bias"_a, "q"_a,
+        "k"_a, "v"_a, "b"_a, "initial_state_source"_a, "initial_state_indices"_a,
+        "cu_seqlens"_a, "scale"_a = std::optional<float>(), "use_qk_l2norm_in_kernel"_a = false,
+        "softplus_beta"_a = 1.0f, "softplus_threshold"_a = 20.0f);
   m.def("npu_chunk_gated_delta_rule", &npu::npu_chunk_gated_delta_rule, "q"_a, "k"_a, "v"_a,
         "g"_a, "beta"_a, "scale"_a = std::optional<float>(), "initial_state"_a = OptT(),
         "output_final_state"_a = false, "cu_seqlens"_a = OptT(), "head_first"_a = false,

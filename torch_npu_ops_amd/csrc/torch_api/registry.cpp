@@ -32,6 +32,9 @@ const Entry kKernels[] = {
     {"layer_norm_fwd_kernel_fast_rms_bf16_z_nobias", reinterpret_cast<void*>(&xk_layer_norm_fwd)},
     {"layer_norm_fwd_kernel_fast_rms_bf16_z_nobias_nomask",
      reinterpret_cast<void*>(&xk_layer_norm_fwd)},
+    {"fused_gdn_gating_decode_kernel", reinterpret_cast<void*>(&xk_fused_gdn_gating)},
+    {"fused_sigmoid_gating_delta_rule_update_kernel",
+     reinterpret_cast<void*>(&xk_gdn_sigmoid_gating_update)},
     {"fused_recurrent_gated_delta_rule_fwd_kernel", reinterpret_cast<void*>(&xk_gdn_recurrent)},
     {"fused_recurrent_gated_delta_rule_spec_fwd_kernel",
      reinterpret_cast<void*>(&xk_gdn_recurrent)},

@@ -353,6 +353,99 @@ std::pair<torch::Tensor, torch::Tensor> npu_fused_recurrent_gated_delta_rule(
   return {o, fin};
 }
 
+// triton_npu/torch_api/npu_triton_fused_gdn_gating.cpp:33-94
+std::pair<torch::Tensor, torch::Tensor> npu_fused_gdn_gating(torch::Tensor& A_log,
+                                                             torch::Tensor& a, torch::Tensor& b,
+                                                             torch::Tensor& dt_bias, float beta,
+                                                             float threshold) {
+  for (auto [t, name] : {std::pair<const torch::Tensor*, const char*>{&A_log, "A_log"},
+                         {&a, "a"}, {&b, "b"}, {&dt_bias, "dt_bias"}}) {
+    TORCH_CHECK(t->defined(), name, " tensor is not defined");
+    TORCH_CHECK(t->is_contiguous(), name, " tensor must be contiguous");
+  }
+  TORCH_CHECK(A_log.scalar_type() == torch::kFloat32, "A_log must be float32");
+  TORCH_CHECK(dt_bias.scalar_type() == torch::kFloat32, "dt_bias must be float32");
+  TORCH_CHECK(A_log.dim() == 1, "A_log must be 1D tensor");
+  TORCH_CHECK(a.dim() == 2, "a must be 2D tensor (batch, num_heads)");
+  TORCH_CHECK(b.dim() == 2, "b must be 2D tensor (batch, num_heads)");
+  TORCH_CHECK(dt_bias.dim() == 1, "dt_bias must be 1D tensor");
+  TORCH_CHECK(a.sizes() == b.sizes() && a.scalar_type() == b.scalar_type(),
+              "a and b must have the same shape and dtype");
+  const int64_t batch = a.size(0), num_heads = a.size(1);
+  auto g = torch::empty({1, batch, num_heads}, a.options().dtype(torch::kFloat32));
+  auto beta_output = torch::empty({1, batch, num_heads}, b.options());
+  check(xk_fused_gdn_gating(static_cast<const float*>(A_log.data_ptr()), a.data_ptr(),
+                            b.data_ptr(), static_cast<const float*>(dt_bias.data_ptr()),
+                            static_cast<float*>(g.data_ptr()), beta_output.data_ptr(), batch,
+                            num_heads, beta, threshold, xdt(a), stream_of(a)),
+        "xk_fused_gdn_gating");
+  return {g, beta_output};
+}
+
+// triton_npu/torch_api/npu_triton_fused_sigmoid_gating_delta_rule_update.cpp:54-177
+torch::Tensor npu_fused_sigmoid_gating_delta_rule_update(
+    torch::Tensor& A_log, torch::Tensor& a, torch::Tensor& dt_bias, torch::Tensor& q,
+    torch::Tensor& k, torch::Tensor& v, torch::Tensor& b, torch::Tensor& initial_state_source,
+    torch::Tensor& initial_state_indices, torch::Tensor& cu_seqlens,
+    const std::optional<float>& scale, bool use_qk_l2norm_in_kernel, float softplus_beta,
+    float softplus_threshold) {
+  for (auto [t, name] : {std::pair<const torch::Tensor*, const char*>{&A_log, "A_log"},
+                         {&a, "a"}, {&dt_bias, "dt_bias"}, {&q, "q"}, {&k, "k"}, {&v, "v"},
+                         {&b, "b"}, {&initial_state_source, "initial_state_source"},
+                         {&initial_state_indices, "initial_state_indices"},
+                         {&cu_seqlens, "cu_seqlens"}}) {
+    TORCH_CHECK(t->defined(), name, " must be defined");
+    TORCH_CHECK(t->is_contiguous(), name, " must be contiguous");
+  }
+  TORCH_CHECK(q.dim() == 4, "q must be 4D [B, T, H, K]");
+  TORCH_CHECK(k.dim() == 4, "k must be 4D [B, T, H, K]");
+  TORCH_CHECK(v.dim() == 4, "v must be 4D [B, T, HV, V]");
+  TORCH_CHECK(a.dim() == 3, "a must be 3D [B, T, HV]");
+  TORCH_CHECK(b.dim() == 3, "b must be 3D [B, T, HV]");
+  TORCH_CHECK(A_log.dim() == 1, "A_log must be 1D [HV]");
+  TORCH_CHECK(dt_bias.dim() == 1, "dt_bias must be 1D [HV]");
+  TORCH_CHECK(initial_state_source.dim() == 4,
+              "initial_state_source must be 4D [slots, HV, K, V]");
+  TORCH_CHECK(initial_state_indices.dim() == 1, "initial_state_indices must be 1D [N]");
+  TORCH_CHECK(cu_seqlens.dim() == 1, "cu_seqlens must be 1D [N + 1]");
+  const int64_t B = k.size(0), T = k.size(1), H = k.size(2), K = k.size(3);
+  const int64_t HV = v.size(2), V = v.size(3);
+  const int64_t N = cu_seqlens.numel() - 1;
+  TORCH_CHECK(q.sizes() == k.sizes(), "q/k shape mismatch");
+  TORCH_CHECK(v.size(0) == B && v.size(1) == T, "v B/T mismatch");
+  TORCH_CHECK(a.size(0) == B && a.size(1) == T && a.size(2) == HV, "a shape mismatch");
+  TORCH_CHECK(b.sizes() == a.sizes(), "a/b shape mismatch");
+  TORCH_CHECK(A_log.numel() == HV, "A_log HV mismatch");
+  TORCH_CHECK(dt_bias.numel() == HV, "dt_bias HV mismatch");
+  TORCH_CHECK(initial_state_source.size(1) == HV && initial_state_source.size(2) == K &&
+                  initial_state_source.size(3) == V,
+              "initial_state_source shape mismatch");
+  TORCH_CHECK(initial_state_indices.numel() == N,
+              "initial_state_indices size must equal cu_seqlens size - 1");
+  TORCH_CHECK(HV % H == 0, "HV must be divisible by H");
+  TORCH_CHECK(A_log.scalar_type() == torch::kFloat32, "A_log must be float32");
+  TORCH_CHECK(dt_bias.scalar_type() == torch::kFloat32, "dt_bias must be float32");
+  TORCH_CHECK(initial_state_source.scalar_type() == torch::kFloat32,
+              "initial_state_source must be float32");
+  TORCH_CHECK(initial_state_indices.scalar_type() == torch::kInt32,
+              "initial_state_indices must be int32");
+  TORCH_CHECK(cu_seqlens.scalar_type() == torch::kInt32, "cu_seqlens must be int32");
+  TORCH_CHECK(a.scalar_type() == b.scalar_type(), "a and b must have the same dtype");
+  const float sc = scale.has_value() ? *scale : 1.0f / std::sqrt(static_cast<float>(K));
+  auto o = torch::empty({B, T, HV, V}, q.options());
+  check(xk_gdn_sigmoid_gating_update(
+            static_cast<const float*>(A_log.data_ptr()), a.data_ptr(),
+            static_cast<const float*>(dt_bias.data_ptr()), softplus_beta, softplus_threshold,
+            q.data_ptr(), k.data_ptr(), v.data_ptr(), b.data_ptr(), xdt(a), o.data_ptr(),
+            static_cast<float*>(initial_state_source.data_ptr()), initial_state_source.stride(0),
+            initial_state_source.size(0),
+            static_cast<const int32_t*>(initial_state_indices.data_ptr()),
+            static_cast<const int32_t*>(cu_seqlens.data_ptr()), N, H, HV, K, V, sc,
+            use_qk_l2norm_in_kernel, xdt(q), stream_of(q)),
+        "xk_gdn_sigmoid_gating_update");
+  return o;
+}
+
 // triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:556-642
 std::pair<torch::Tensor, torch::Tensor> npu_chunk_gated_delta_rule(
     torch::Tensor& q, torch::Tensor& k, torch::Tensor& v, torch::Tensor& g, torch::Tensor& beta,

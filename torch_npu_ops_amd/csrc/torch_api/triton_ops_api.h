@@ -13,9 +13,8 @@
 //    (split_rmsnorm_rope, l2norm);
 //  * the chunked op runs its whole pipeline on the device without reading
 //    cu_seqlens on the host.
-// rope_inplace, npu_fused_gdn_gating, npu_fused_sigmoid_gating_delta_rule_update
-// and npu_fused_qkvzba_split_reshape_cat of the reference header are outside
-// this build's op set and are not declared.
+// rope_inplace and npu_fused_qkvzba_split_reshape_cat of the reference
+// header are outside this build's op set and are not declared.
 #pragma once
 
 #include <torch/torch.h>
@@ -50,6 +49,12 @@ torch::Tensor npu_chunk_fwd_o(const torch::Tensor& q, const torch::Tensor& k,
                               const torch::Tensor& g_cumsum, float scale, int64_t chunk_size,
                               const std::optional<torch::Tensor>& cu_seqlens);
 
+std::pair<torch::Tensor, torch::Tensor> npu_fused_gdn_gating(torch::Tensor& A_log,
+                                                             torch::Tensor& a, torch::Tensor& b,
+                                                             torch::Tensor& dt_bias,
+                                                             float beta = 1.0f,
+                                                             float threshold = 20.0f);
+
 std::pair<torch::Tensor, torch::Tensor> npu_fused_recurrent_gated_delta_rule(
     torch::Tensor& q, torch::Tensor& k, torch::Tensor& v, torch::Tensor& g,
     const std::optional<torch::Tensor>& beta = std::nullopt,
@@ -60,6 +65,13 @@ std::pair<torch::Tensor, torch::Tensor> npu_fused_recurrent_gated_delta_rule(
     const std::optional<torch::Tensor>& ssm_state_indices = std::nullopt,
     const std::optional<torch::Tensor>& num_accepted_tokens = std::nullopt,
     bool use_qk_l2norm_in_kernel = false);
+
+torch::Tensor npu_fused_sigmoid_gating_delta_rule_update(
+    torch::Tensor& A_log, torch::Tensor& a, torch::Tensor& dt_bias, torch::Tensor& q,
+    torch::Tensor& k, torch::Tensor& v, torch::Tensor& b, torch::Tensor& initial_state_source,
+    torch::Tensor& initial_state_indices, torch::Tensor& cu_seqlens,
+    const std::optional<float>& scale = std::nullopt, bool use_qk_l2norm_in_kernel = false,
+    float softplus_beta = 1.0f, float softplus_threshold = 20.0f);
 
 std::pair<torch::Tensor, torch::Tensor> npu_chunk_gated_delta_rule(
     torch::Tensor& q, torch::Tensor& k, torch::Tensor& v, torch::Tensor& g, torch::Tensor& beta,

@@ -391,6 +391,103 @@ def npu_fused_recurrent_gated_delta_rule(
     return o, final
 
 
+def npu_fused_gdn_gating(A_log: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
+                         dt_bias: torch.Tensor, beta: float = 1.0,
+                         threshold: float = 20.0):
+    """GDN gating; returns (g [1, batch, heads] fp32, beta_output [1, batch,
+    heads] in b's dtype).
+
+    Mirrors npu_fused_gdn_gating
+    (triton_npu/torch_api/npu_triton_fused_gdn_gating.cpp:33-94):
+    g = -exp(A_log) * softplus_{beta, threshold}(a + dt_bias),
+    beta_output = sigmoid(b); A_log and dt_bias are fp32 [heads], a and b
+    [batch, heads].
+    """
+    for t, name in ((A_log, "A_log"), (a, "a"), (b, "b"), (dt_bias, "dt_bias")):
+        if not t.is_contiguous():
+            raise ValueError(f"{name} tensor must be contiguous")
+    if A_log.dtype != torch.float32:
+        raise ValueError("A_log must be float32")
+    if dt_bias.dtype != torch.float32:
+        raise ValueError("dt_bias must be float32")
+    if A_log.dim() != 1 or dt_bias.dim() != 1:
+        raise ValueError("A_log and dt_bias must be 1D tensors")
+    if a.dim() != 2 or b.dim() != 2:
+        raise ValueError("a and b must be 2D tensors (batch, num_heads)")
+    if b.dtype != a.dtype or b.shape != a.shape:
+        raise ValueError("a and b must have the same dtype and shape")
+    batch, heads = a.shape
+    g = torch.empty(1, batch, heads, dtype=torch.float32, device=a.device)
+    beta_out = torch.empty(1, batch, heads, dtype=b.dtype, device=b.device)
+    st = lib().xk_fused_gdn_gating(A_log.data_ptr(), a.data_ptr(), b.data_ptr(),
+                                   dt_bias.data_ptr(), g.data_ptr(), beta_out.data_ptr(),
+                                   batch, heads, float(beta), float(threshold),
+                                   xk_dtype(a), _stream(a))
+    check(st, "xk_fused_gdn_gating")
+    return g, beta_out
+
+
+def npu_fused_sigmoid_gating_delta_rule_update(
+        A_log: torch.Tensor, a: torch.Tensor, dt_bias: torch.Tensor, q: torch.Tensor,
+        k: torch.Tensor, v: torch.Tensor, b: torch.Tensor,
+        initial_state_source: torch.Tensor, initial_state_indices: torch.Tensor,
+        cu_seqlens: torch.Tensor, scale: Optional[float] = None,
+        use_qk_l2norm_in_kernel: bool = False, softplus_beta: float = 1.0,
+        softplus_threshold: float = 20.0):
+    """Recurrent gated delta rule with in-kernel gating; returns o [B, T,
+    HV, V] and updates initial_state_source in place.
+
+    Mirrors npu_fused_sigmoid_gating_delta_rule_update
+    (triton_npu/torch_api/npu_triton_fused_sigmoid_gating_delta_rule_update.cpp:54-177):
+    q, k [B, T, H, K], v [B, T, HV, V], a, b [B, T, HV], A_log, dt_bias fp32
+    [HV], initial_state_source fp32 [slots, HV, K, V], initial_state_indices
+    int32 [N], cu_seqlens int32 [N + 1].  A negative state index starts from
+    zeros and leaves the pool untouched.
+    """
+    named = ((A_log, "A_log"), (a, "a"), (dt_bias, "dt_bias"), (q, "q"), (k, "k"),
+             (v, "v"), (b, "b"), (initial_state_source, "initial_state_source"),
+             (initial_state_indices, "initial_state_indices"), (cu_seqlens, "cu_seqlens"))
+    for t, name in named:
+        if not t.is_contiguous():
+            raise ValueError(f"{name} tensor must be contiguous")
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q/k must be 4D [B, T, H, K] and v 4D [B, T, HV, V]")
+    B, T, H, K = k.shape
+    HV, V = v.shape[2], v.shape[3]
+    N = cu_seqlens.numel() - 1
+    if q.shape != k.shape:
+        raise ValueError("q/k shape mismatch")
+    if a.shape != (B, T, HV) or b.shape != a.shape:
+        raise ValueError("a/b shape mismatch")
+    if A_log.numel() != HV or dt_bias.numel() != HV:
+        raise ValueError("A_log / dt_bias HV mismatch")
+    if tuple(initial_state_source.shape[1:]) != (HV, K, V):
+        raise ValueError("initial_state_source shape mismatch")
+    if initial_state_indices.numel() != N:
+        raise ValueError("initial_state_indices size must equal cu_seqlens size - 1")
+    if HV % H != 0:
+        raise ValueError("HV must be divisible by H")
+    if A_log.dtype != torch.float32 or dt_bias.dtype != torch.float32:
+        raise ValueError("A_log and dt_bias must be float32")
+    if initial_state_source.dtype != torch.float32:
+        raise ValueError("initial_state_source must be float32")
+    if initial_state_indices.dtype != torch.int32 or cu_seqlens.dtype != torch.int32:
+        raise ValueError("initial_state_indices and cu_seqlens must be int32")
+    if b.dtype != a.dtype:
+        raise ValueError("a and b must have the same dtype")
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(K)
+    o = torch.empty(B, T, HV, V, dtype=q.dtype, device=q.device)
+    st = lib().xk_gdn_sigmoid_gating_update(
+        A_log.data_ptr(), a.data_ptr(), dt_bias.data_ptr(), float(softplus_beta),
+        float(softplus_threshold), q.data_ptr(), k.data_ptr(), v.data_ptr(), b.data_ptr(),
+        xk_dtype(a), o.data_ptr(), initial_state_source.data_ptr(),
+        initial_state_source.stride(0), initial_state_source.size(0),
+        initial_state_indices.data_ptr(), cu_seqlens.data_ptr(), N, H, HV, K, V, sc,
+        int(use_qk_l2norm_in_kernel), xk_dtype(q), _stream(q))
+    check(st, "xk_gdn_sigmoid_gating_update")
+    return o
+
+
 def npu_chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                g: torch.Tensor, beta: torch.Tensor,
                                scale: Optional[float] = None,
