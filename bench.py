@@ -153,6 +153,50 @@ class GemmaCase(Case):
                 "full config 2b (16384x4096), fp32 math on bf16 input", 1.0)
 
 
+class GatedRmsNormCase(Case):
+    name = "gated_rms_norm"
+    config = ("next row (layer_norm_fwd gated RMSNorm epilogue, the reference's nomask "
+              "kernel shape): GDN output of the prefill config as rows of one head, "
+              "x and z bf16 [524288, 128] (16384 tokens x 32 heads), group_size 128, "
+              "RMS, gate z*sigmoid(z) after the norm, no bias, eps 1e-6; outputs y + "
+              "fp32 rstd")
+    kernel = "ln_tile_kernel"
+    M, N = 524288, 128
+    # x, z, y (bf16) + rstd (fp32) + weight
+    algo_bytes = M * N * 2 * 3 + M * 4 + N * 2
+
+    def __init__(self):
+        g = torch.Generator().manual_seed(0)
+        self.x = _randn((self.M, self.N), g, torch.bfloat16)
+        self.z = _randn((self.M, self.N), g, torch.bfloat16)
+        self.w = _randn((self.N,), g, torch.bfloat16, 0.1, 1.0)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        w = self.w.to(dev)
+        out = []
+        for _ in range(n):
+            x, z = self.x.to(dev), self.z.to(dev)
+            y = torch.empty_like(x)
+            rstd = torch.empty(self.M, dtype=torch.float32, device=dev)
+
+            def run(x=x, z=z, y=y, rstd=rstd):
+                _ok(lib.xk_layer_norm_fwd(
+                    x.data_ptr(), self.N, y.data_ptr(), self.N, w.data_ptr(), None,
+                    z.data_ptr(), self.N, None, rstd.data_ptr(), self.M, self.N, self.N,
+                    1e-6, 1, 1, _lib.XK_BF16, _lib.XK_BF16, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import norm as on
+        x, z, w = self.x, self.z, self.w
+        return (lambda: on.layer_norm_fwd(x, w, None, 1e-6, z=z, group_size=128,
+                                          norm_before_gate=True, is_rms_norm=True),
+                "full shape (524288 x 128), fp32 math on bf16 input", 1.0)
+
+
 class RopeCase(Case):
     name = "split_rmsnorm_rope"
     config = ("config 1: split q/k RMSNorm + neox RoPE fp32, 256 tokens, 32 q + "
@@ -613,7 +657,8 @@ class GdnChunkCase(Case):
 
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
                              ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase,
-                             GdnChunkCase, GdnGatingCase, GdnSigmoidGatingCase)}
+                             GdnChunkCase, GdnGatingCase, GdnSigmoidGatingCase,
+                             GatedRmsNormCase)}
 HEADLINE = "layer_norm_fwd"
 
 

@@ -80,6 +80,52 @@ def test_layer_norm_shapes(dev, M, N, G, dtype):
             torch.testing.assert_close(mean.cpu(), rmean, **STAT_TOL)
 
 
+@pytest.mark.parametrize("G,dtype", [
+    (16, torch.bfloat16), (40, torch.bfloat16), (64, torch.bfloat16), (96, torch.bfloat16),
+    (128, torch.bfloat16), (256, torch.bfloat16), (512, torch.bfloat16),
+    (16, torch.float32), (64, torch.float32), (128, torch.float32), (256, torch.float32),
+])
+def test_layer_norm_narrow_groups(dev, G, dtype):
+    # Every narrow-group team shape (4 / 8 / 16 / 32 lanes x 2 vectors),
+    # full and masked, with and without the gate on either side of the norm.
+    from torch_npu_ops_amd import ops
+    gen = torch.Generator().manual_seed(G)
+    M, N = 300, 3 * G
+    x = _rand((M, N), gen, dtype, 2.0, 0.3)
+    z = _rand((M, N), gen, dtype)
+    w = _rand((N,), gen, dtype, 0.1, 1.0)
+    for rms, gate, zz in ((False, True, None), (True, True, z), (True, False, z)):
+        ref, rmean, rrstd = on.layer_norm_fwd(x, w, None, 1e-6, z=zz, group_size=G,
+                                              norm_before_gate=gate, is_rms_norm=rms)
+        y, mean, rstd = ops.layer_norm_fwd(x.to(dev), w.to(dev), None, 1e-6,
+                                           z=zz.to(dev) if zz is not None else None,
+                                           group_size=G, norm_before_gate=gate,
+                                           is_rms_norm=rms, return_stats=True)
+        torch.testing.assert_close(y.float().cpu(), ref, **_tol(dtype))
+        torch.testing.assert_close(rstd.cpu(), rrstd, **STAT_TOL)
+        if not rms:
+            torch.testing.assert_close(mean.cpu(), rmean, **STAT_TOL)
+
+
+def test_gated_rms_norm_epilogue(dev):
+    # The GDN output norm (the reference's nomask kernel shape,
+    # test_layernorm_fwd.py:1614-1638, scaled up): rows of one 128-wide
+    # head, RMS, gate applied after the norm, no bias, bf16.
+    from torch_npu_ops_amd import ops
+    gen = torch.Generator().manual_seed(9)
+    M = 131072
+    x = _rand((M, 128), gen, torch.bfloat16, 0.5)
+    z = _rand((M, 128), gen, torch.bfloat16, 0.5)
+    w = _rand((128,), gen, torch.bfloat16, 0.5)
+    ref, _, rrstd = on.layer_norm_fwd(x, w, None, 1e-6, z=z, group_size=128,
+                                      norm_before_gate=True, is_rms_norm=True)
+    y, _, rstd = ops.layer_norm_fwd(x.to(dev), w.to(dev), None, 1e-6, z=z.to(dev),
+                                    group_size=128, norm_before_gate=True, is_rms_norm=True,
+                                    return_stats=True)
+    torch.testing.assert_close(y.float().cpu(), ref, **BF16_TOL)
+    torch.testing.assert_close(rstd.cpu(), rrstd, **STAT_TOL)
+
+
 def test_layer_norm_strided_rows(dev):
     from torch_npu_ops_amd import ops
     gen = torch.Generator().manual_seed(8)
