@@ -583,6 +583,48 @@ class GdnSigmoidGatingCase(Case):
         return run, f"{n} of 256 sequences, fp32", a.B / n
 
 
+class QkvzbaSplitCase(Case):
+    name = "qkvzba_split"
+    config = ("next row (npu_fused_qkvzba_split_reshape_cat) on the prefill shape: "
+              "16384 rows, 16 qk / 32 v heads (2 per qk head), head dims 128, bf16 "
+              "mixed_qkvz [16384, 12288] and mixed_ba [16384, 64]")
+    kernel = "qkvzba_split_kernel"
+    R, NQK, NV, HD = 16384, 16, 32, 128
+    W = NQK * (2 * HD + 2 * (NV // NQK) * HD)
+    # every element read once and written once (bf16)
+    algo_bytes = R * (W + 2 * NV) * 2 * 2
+
+    def __init__(self):
+        g = torch.Generator().manual_seed(0)
+        self.qkvz = _randn((self.R, self.W), g, torch.bfloat16)
+        self.ba = _randn((self.R, 2 * self.NV), g, torch.bfloat16)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        out = []
+        qkv_dim = 2 * self.NQK * self.HD + self.NV * self.HD
+        for _ in range(n):
+            qkvz, ba = self.qkvz.to(dev), self.ba.to(dev)
+            qkv = torch.empty(self.R, qkv_dim, dtype=torch.bfloat16, device=dev)
+            z = torch.empty(self.R, self.NV * self.HD, dtype=torch.bfloat16, device=dev)
+            b = torch.empty(self.R, self.NV, dtype=torch.bfloat16, device=dev)
+            a = torch.empty_like(b)
+
+            def run(qkvz=qkvz, ba=ba, qkv=qkv, z=z, b=b, a=a):
+                _ok(lib.xk_fused_qkvzba_split_reshape_cat(
+                    qkvz.data_ptr(), self.W, ba.data_ptr(), 2 * self.NV, qkv.data_ptr(),
+                    z.data_ptr(), b.data_ptr(), a.data_ptr(), self.R, self.NQK, self.NV,
+                    self.HD, self.HD, _lib.XK_BF16, _lib.XK_BF16, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import layout as ol
+        a = (self.qkvz, self.ba, self.NQK, self.NV, self.HD, self.HD)
+        return (lambda: ol.fused_qkvzba_split_reshape_cat(*a), "full shape, copies", 1.0)
+
+
 def chunk_gdn_flops(tokens, HV, K=128, V=128, C=64):
     """Algorithmic FLOPs of the chunked gated delta rule per call, summed
     per 64-token chunk and v-head: K K^T, Q K^T (2C^2K each), W = A(k b e^g)
@@ -658,7 +700,7 @@ class GdnChunkCase(Case):
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
                              ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase,
                              GdnChunkCase, GdnGatingCase, GdnSigmoidGatingCase,
-                             GatedRmsNormCase)}
+                             GatedRmsNormCase, QkvzbaSplitCase)}
 HEADLINE = "layer_norm_fwd"
 
 

@@ -241,6 +241,25 @@ int xk_gdn_sigmoid_gating_update(
     int use_qk_l2norm, xk_dtype dtype, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Split of the GDN input projection (the step before the conv1d).
+ * Replaces xllm::kernel::npu::npu_fused_qkvzba_split_reshape_cat
+ *   (triton_npu/torch_api/triton_ops_api.h:178-184,
+ *    npu_triton_fused_qkvzba_split_reshape.cpp:116-230; kernels
+ *    triton_src/test_fused_qkvzba_split_reshape.py:31-351).
+ *   R = num_heads_v / num_heads_qk.  Each row of mixed_qkvz holds
+ *   num_heads_qk groups [q (head_qk) | k (head_qk) | v (R*head_v) |
+ *   z (R*head_v)]; each row of mixed_ba holds groups [b (R) | a (R)].
+ *   Outputs (dense rows): mixed_qkv [rows, 2*num_heads_qk*head_qk +
+ *   num_heads_v*head_v] = [all q | all k | all v], z [rows, num_heads_v *
+ *   head_v], b and a [rows, num_heads_v].  A permutation: exact copies.
+ */
+int xk_fused_qkvzba_split_reshape_cat(
+    const void* mixed_qkvz, int64_t stride_qkvz_row, const void* mixed_ba,
+    int64_t stride_ba_row, void* mixed_qkv, void* z, void* b, void* a, int64_t rows,
+    int64_t num_heads_qk, int64_t num_heads_v, int64_t head_qk, int64_t head_v,
+    xk_dtype dtype, xk_dtype ba_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
  * a8. One decode step of the gated delta rule fused with the causal conv1d
  * update of its mixed q/k/v projection (no single reference function: the
  * composition of npu_causal_conv1d_update, the [q | k | v] channel split of

@@ -26,13 +26,14 @@ def test_registry_maps_reference_names_to_entry_points(xt):
         "split_rmsnorm_rope_kernel": "xk_split_rmsnorm_rope",
         "fused_gdn_gating_decode_kernel": "xk_fused_gdn_gating",
         "fused_sigmoid_gating_delta_rule_update_kernel": "xk_gdn_sigmoid_gating_update",
+        "fused_qkvzba_split_reshape_cat_gqa_r3_kernel": "xk_fused_qkvzba_split_reshape_cat",
     }
     for name, sym in pairs.items():
         assert xt.registry_register(name, "/path/ignored.npubin")
         assert xt.registry_stub(name) == ctypes.cast(getattr(lib, sym), ctypes.c_void_p).value
     # kernels outside the op set are not registered
     assert not xt.registry_register("rope_inplace_kernel", "")
-    assert xt.registry_stub("fused_qkvzba_split_reshape_cat_gqa_r1_kernel") == 0
+    assert xt.registry_stub("_causal_conv1d_update_kernel_no_cache_len") == 0
 
 
 def test_factory_names_and_status_forwarding(xt):

@@ -57,6 +57,8 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "xk_gdn_sigmoid_gating_update": (
         [P, P, P, F32, F32, P, P, P, P, INT, P, P, I64, I64, P, P, I64, I64, I64,
          I64, I64, F32, INT, INT, P], INT),
+    "xk_fused_qkvzba_split_reshape_cat": (
+        [P, I64, P, I64, P, P, P, P, I64, I64, I64, I64, I64, INT, INT, P], INT),
     "xk_gdn_conv_decode": (
         [P, I64, P, I64, I64, I64, I64, I64, P, I64, I64, P, INT, I64, P, I32,
          P, INT, P, INT, P, I64, I64, P, P, I64, I64, I64, I64, I64, F32, INT,

@@ -72,6 +72,10 @@ XK_OPERATION(CausalConv1dUpdateNoCacheNoMtpOp, xk_causal_conv1d_update);
 XK_OPERATION(CausalConv1dUpdateQwenDecodeOp, xk_causal_conv1d_update);
 XK_OPERATION(CausalConv1dUpdateTiledV2Op, xk_causal_conv1d_varlen);
 XK_OPERATION(SplitRmsnormRopeOp, xk_split_rmsnorm_rope);
+XK_OPERATION(FusedQkvzbaSplitReshapeGqaR1Op, xk_fused_qkvzba_split_reshape_cat);
+XK_OPERATION(FusedQkvzbaSplitReshapeGqaR2Op, xk_fused_qkvzba_split_reshape_cat);
+XK_OPERATION(FusedQkvzbaSplitReshapeGqaR3Op, xk_fused_qkvzba_split_reshape_cat);
+XK_OPERATION(FusedQkvzbaSplitReshapeGqaR4Op, xk_fused_qkvzba_split_reshape_cat);
 // No reference counterpart: the whole chunked pipeline and the fused decode step.
 XK_OPERATION(ChunkGatedDeltaRuleFusedOp, xk_gdn_chunk_fwd);
 XK_OPERATION(GdnConvDecodeOp, xk_gdn_conv_decode);

@@ -42,6 +42,9 @@ PYBIND11_MODULE(_xk_torch, m) {
         "k"_a, "v"_a, "b"_a, "initial_state_source"_a, "initial_state_indices"_a,
         "cu_seqlens"_a, "scale"_a = std::optional<float>(), "use_qk_l2norm_in_kernel"_a = false,
         "softplus_beta"_a = 1.0f, "softplus_threshold"_a = 20.0f);
+  m.def("npu_fused_qkvzba_split_reshape_cat", &npu::npu_fused_qkvzba_split_reshape_cat,
+        "mixed_qkvz"_a, "mixed_ba"_a, "num_heads_qk"_a, "num_heads_v"_a, "head_qk"_a,
+        "head_v"_a);
   m.def("npu_chunk_gated_delta_rule", &npu::npu_chunk_gated_delta_rule, "q"_a, "k"_a, "v"_a,
         "g"_a, "beta"_a, "scale"_a = std::optional<float>(), "initial_state"_a = OptT(),
         "output_final_state"_a = false, "cu_seqlens"_a = OptT(), "head_first"_a = false,

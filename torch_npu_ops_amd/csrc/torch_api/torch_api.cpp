@@ -50,6 +50,12 @@ torch::Tensor rows(const torch::Tensor& x, int64_t N) {
   return x2.stride(-1) == 1 ? x2 : x2.contiguous();
 }
 
+// x as [rows, -1] with unit column stride (a copy only if needed).
+torch::Tensor rows_of(const torch::Tensor& x, int64_t rows) {
+  auto x2 = x.reshape({rows, -1});
+  return x2.stride(-1) == 1 ? x2 : x2.contiguous();
+}
+
 // cu_seqlens on the device (int32/int64 kept), or B sequences of T tokens.
 std::pair<torch::Tensor, int64_t> seqs(int64_t B, int64_t T,
                                        const std::optional<torch::Tensor>& cu_seqlens,
@@ -444,6 +450,36 @@ torch::Tensor npu_fused_sigmoid_gating_delta_rule_update(
             use_qk_l2norm_in_kernel, xdt(q), stream_of(q)),
         "xk_gdn_sigmoid_gating_update");
   return o;
+}
+
+// triton_npu/torch_api/npu_triton_fused_qkvzba_split_reshape.cpp:116-230
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor>
+npu_fused_qkvzba_split_reshape_cat(torch::Tensor& mixed_qkvz, torch::Tensor& mixed_ba,
+                                   int32_t num_heads_qk, int32_t num_heads_v, int32_t head_qk,
+                                   int32_t head_v) {
+  const int64_t rows = mixed_qkvz.size(0);
+  const int32_t v_heads_per_qk = num_heads_v / num_heads_qk;
+  TORCH_CHECK(v_heads_per_qk >= 1 && v_heads_per_qk <= 4 && num_heads_v % num_heads_qk == 0,
+              "npu_fused_qkvzba_split_reshape_cat only supports v_heads_per_qk in [1, 4], "
+              "but got ", v_heads_per_qk, " for num_heads_qk=", num_heads_qk,
+              " num_heads_v=", num_heads_v);
+  auto q2 = rows_of(mixed_qkvz, rows);
+  auto b2 = rows_of(mixed_ba, rows);
+  const int64_t qkv_dim = static_cast<int64_t>(num_heads_qk) * head_qk * 2 +
+                          static_cast<int64_t>(num_heads_v) * head_v;
+  auto mixed_qkv = torch::empty({rows, qkv_dim}, mixed_qkvz.options());
+  auto z_flat = torch::empty({rows, static_cast<int64_t>(num_heads_v) * head_v},
+                             mixed_qkvz.options());
+  auto b = torch::empty({rows, num_heads_v}, mixed_ba.options());
+  auto a = torch::empty({rows, num_heads_v}, mixed_ba.options());
+  check(xk_fused_qkvzba_split_reshape_cat(q2.data_ptr(), q2.stride(0), b2.data_ptr(),
+                                          b2.stride(0), mixed_qkv.data_ptr(), z_flat.data_ptr(),
+                                          b.data_ptr(), a.data_ptr(), rows, num_heads_qk,
+                                          num_heads_v, head_qk, head_v, xdt(q2), xdt(b2),
+                                          stream_of(mixed_qkvz)),
+        "xk_fused_qkvzba_split_reshape_cat");
+  auto z = z_flat.view({rows, num_heads_v, head_v});
+  return {mixed_qkv, z, b, a};
 }
 
 // triton_npu/torch_api/npu_triton_chunk_gated_delta_rule.cpp:556-642

@@ -13,8 +13,8 @@
 //    (split_rmsnorm_rope, l2norm);
 //  * the chunked op runs its whole pipeline on the device without reading
 //    cu_seqlens on the host.
-// rope_inplace and npu_fused_qkvzba_split_reshape_cat of the reference
-// header are outside this build's op set and are not declared.
+// rope_inplace of the reference header is outside this build's op set and
+// is not declared.
 #pragma once
 
 #include <torch/torch.h>
@@ -115,6 +115,11 @@ torch::Tensor npu_causal_conv1d_update_v2(
     const std::optional<torch::Tensor>& initial_state_idx = std::nullopt,
     bool validate_data = false,
     const std::optional<torch::Tensor>& num_accepted_tokens = std::nullopt);
+
+std::tuple<torch::Tensor, torch::Tensor, torch::Tensor, torch::Tensor>
+npu_fused_qkvzba_split_reshape_cat(torch::Tensor& mixed_qkvz, torch::Tensor& mixed_ba,
+                                   int32_t num_heads_qk, int32_t num_heads_v, int32_t head_qk,
+                                   int32_t head_v);
 
 std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> npu_split_rmsnorm_rope(
     torch::Tensor& input, torch::Tensor& sin, torch::Tensor& cos, torch::Tensor& q_weight,

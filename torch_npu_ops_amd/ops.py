@@ -488,6 +488,42 @@ def npu_fused_sigmoid_gating_delta_rule_update(
     return o
 
 
+def npu_fused_qkvzba_split_reshape_cat(mixed_qkvz: torch.Tensor, mixed_ba: torch.Tensor,
+                                       num_heads_qk: int, num_heads_v: int, head_qk: int,
+                                       head_v: int):
+    """Split of the GDN input projection; returns (mixed_qkv, z [rows,
+    num_heads_v, head_v], b, a).
+
+    Mirrors npu_fused_qkvzba_split_reshape_cat
+    (triton_npu/torch_api/npu_triton_fused_qkvzba_split_reshape.cpp:116-230):
+    rows of mixed_qkvz hold per-qk-head groups [q | k | v | z] and rows of
+    mixed_ba groups [b | a]; v heads per qk head must be in [1, 4].
+    """
+    rph = num_heads_v // num_heads_qk
+    if not (1 <= rph <= 4) or num_heads_v % num_heads_qk:
+        raise ValueError(
+            "npu_fused_qkvzba_split_reshape_cat only supports v_heads_per_qk in [1, 4], "
+            f"but got {rph} for num_heads_qk={num_heads_qk} num_heads_v={num_heads_v}")
+    rows = mixed_qkvz.size(0)
+    qkv_dim = num_heads_qk * head_qk * 2 + num_heads_v * head_v
+    q2 = mixed_qkvz.reshape(rows, -1)
+    b2 = mixed_ba.reshape(rows, -1)
+    if q2.stride(-1) != 1:
+        q2 = q2.contiguous()
+    if b2.stride(-1) != 1:
+        b2 = b2.contiguous()
+    mixed_qkv = torch.empty(rows, qkv_dim, dtype=mixed_qkvz.dtype, device=mixed_qkvz.device)
+    z = torch.empty(rows, num_heads_v * head_v, dtype=mixed_qkvz.dtype, device=mixed_qkvz.device)
+    b = torch.empty(rows, num_heads_v, dtype=mixed_ba.dtype, device=mixed_ba.device)
+    a = torch.empty(rows, num_heads_v, dtype=mixed_ba.dtype, device=mixed_ba.device)
+    st = lib().xk_fused_qkvzba_split_reshape_cat(
+        q2.data_ptr(), q2.stride(0), b2.data_ptr(), b2.stride(0), mixed_qkv.data_ptr(),
+        z.data_ptr(), b.data_ptr(), a.data_ptr(), rows, num_heads_qk, num_heads_v, head_qk,
+        head_v, xk_dtype(q2), xk_dtype(b2), _stream(mixed_qkvz))
+    check(st, "xk_fused_qkvzba_split_reshape_cat")
+    return mixed_qkv, z.view(rows, num_heads_v, head_v), b, a
+
+
 def npu_chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                g: torch.Tensor, beta: torch.Tensor,
                                scale: Optional[float] = None,
