@@ -6,9 +6,10 @@
 One step = one call of an op on its BASELINE config with inputs already
 resident in HBM.  HIP events on the stream the kernels run on bracket the K
 timed calls, launched back to back.  Ops that move >= 100 MB per call are
-launched eagerly (the GPU queue stays ahead of the Python binding); the two
-microsecond-scale ops (configs 1 and 3b), whose kernels are shorter than a
-Python launch, are captured in one HIP graph that is replayed.  Inputs
+launched eagerly (the GPU queue stays ahead of the Python binding); the
+smaller ops (configs 1 and 3b, and the gating / in-place RoPE lines), whose
+kernels are not much longer than a Python launch, are captured in one HIP
+graph that is replayed.  Inputs
 rotate over several buffer sets whose total exceeds the 256 MB Infinity
 Cache, so timings see HBM.
 
@@ -195,6 +196,44 @@ class GatedRmsNormCase(Case):
         return (lambda: on.layer_norm_fwd(x, w, None, 1e-6, z=z, group_size=128,
                                           norm_before_gate=True, is_rms_norm=True),
                 "full shape (524288 x 128), fp32 math on bf16 input", 1.0)
+
+
+class RopeInplaceCase(Case):
+    name = "rope_inplace"
+    config = ("next row (rope_inplace, GPT-J interleaved partial RoPE): x bf16 "
+              "[16384, 16, 512] rotated in place on its last 64 elements, sin / cos "
+              "bf16 [16384, 64]")
+    kernel = "rope_inplace_kernel"
+    timing = "graph"
+    T, H, HID, RD = 16384, 16, 512, 64
+    # rope part of x read + written, sin / cos read (bf16)
+    algo_bytes = T * H * RD * 2 * 2 + 2 * T * RD * 2
+
+    def __init__(self):
+        g = torch.Generator().manual_seed(0)
+        self.x = _randn((self.T, self.H, self.HID), g, torch.bfloat16)
+        self.sin = _randn((self.T, self.RD), g, torch.bfloat16)
+        self.cos = _randn((self.T, self.RD), g, torch.bfloat16)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        out = []
+        for _ in range(n):
+            x, sin, cos = self.x.to(dev), self.sin.to(dev), self.cos.to(dev)
+
+            def run(x=x, sin=sin, cos=cos):
+                _ok(lib.xk_rope_inplace(x.data_ptr(), self.T * self.H, self.H, self.HID,
+                                        self.HID, sin.data_ptr(), cos.data_ptr(), self.RD,
+                                        self.RD, _lib.XK_BF16, _lib.XK_BF16,
+                                        _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import rope as orp
+        a = (self.x, self.sin, self.cos, self.RD)
+        return (lambda: orp.rope_inplace_ref(*a), "full shape, fp32 math", 1.0)
 
 
 class RopeCase(Case):
@@ -700,7 +739,7 @@ class GdnChunkCase(Case):
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
                              ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase,
                              GdnChunkCase, GdnGatingCase, GdnSigmoidGatingCase,
-                             GatedRmsNormCase, QkvzbaSplitCase)}
+                             GatedRmsNormCase, QkvzbaSplitCase, RopeInplaceCase)}
 HEADLINE = "layer_norm_fwd"
 
 

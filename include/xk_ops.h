@@ -115,6 +115,24 @@ int xk_split_rmsnorm_rope(const void* qkv, int64_t stride_qkv_row,
                           void* stream);
 
 /* ------------------------------------------------------------------------
+ * In-place GPT-J (interleaved) RoPE on the last rope_dim elements of rows.
+ * Replaces xllm::kernel::npu::rope_inplace
+ *   (triton_npu/torch_api/triton_ops_api.h:68-71,
+ *    npu_triton_rope_inplace.cpp:22-64; kernel
+ *    triton_src/test_rope_inplace.py:17-49).
+ *   x : rows of `hidden` elements (row stride stride_x_row), updated in
+ *   place; row r uses sin / cos row r / head_num ([*, >= rope_dim], row stride
+ *   stride_sc_row, in sc_dtype = dtype or fp32).  With d = hidden - rope_dim:
+ *     x[d+2i]   <- x[d+2i] cos[2i] - x[d+2i+1] sin[2i]
+ *     x[d+2i+1] <- x[d+2i+1] cos[2i+1] + x[d+2i] sin[2i+1]
+ *   rope_dim even; offsets and strides even.
+ */
+int xk_rope_inplace(void* x, int64_t rows, int64_t head_num, int64_t stride_x_row,
+                    int64_t hidden, const void* sin, const void* cos,
+                    int64_t stride_sc_row, int64_t rope_dim, xk_dtype dtype,
+                    xk_dtype sc_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
  * a4. Depthwise causal conv1d state update (decode / short MTP windows).
  * Replaces xllm::kernel::npu::npu_causal_conv1d_update
  *   (triton_npu/torch_api/triton_ops_api.h:147-160,

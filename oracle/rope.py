@@ -11,9 +11,15 @@ neox_cos_sin builds the per-token cos/sin rows the way the reference's ATB
 rope consumes a neox cos_sin_cache (ops_npu/rope_atb.cpp:16-23):
 freqs = pos * inv_freq, cos = cat(cos f, cos f), sin = cat(sin f, sin f).
 
+rope_inplace_ref restates rope_ref of triton_npu/triton_src/
+test_rope_inplace.py:66-94: GPT-J (interleaved) rotation of the last
+rope_dim elements, out = x*cos + rotate(x)*sin with rotate(x)[2i] = -x[2i+1]
+and rotate(x)[2i+1] = x[2i], rounded to x's dtype.
+
 Pins (tests/test_oracle_rope.py): F.rms_norm for the norm, a complex-number
-rotation (x1 + i x2)(cos + i sin) for the rotate-half sign convention,
-pair-norm preservation, and position 0 reducing to the plain norm.
+rotation (x1 + i x2)(cos + i sin) for the rotate-half sign convention and
+(x[2i] + i x[2i+1])(cos + i sin) for the interleaved one, pair-norm
+preservation, and position 0 (cos 1, sin 0) reducing to the identity.
 """
 from __future__ import annotations
 
@@ -66,3 +72,20 @@ def split_rmsnorm_rope(qkv: torch.Tensor, sin: torch.Tensor, cos: torch.Tensor,
     qo = qn * c + _rotate_half(qn) * s
     ko = kn * c + _rotate_half(kn) * s
     return qo.reshape(T, q_hidden), ko.reshape(T, kv_hidden), v.to(dtype)
+
+
+def rope_inplace_ref(x: torch.Tensor, sin: torch.Tensor, cos: torch.Tensor,
+                     rope_dim: int) -> torch.Tensor:
+    """x [bsz, hidden] or [bsz, heads, hidden]; sin / cos [bsz, rope_dim].
+    Returns the rotated copy of x (same dtype; the prefix is unchanged)."""
+    orig = x.dtype
+    pre = x[..., :-rope_dim] if rope_dim < x.shape[-1] else None
+    xr = x[..., -rope_dim:].float()
+    s, c = sin.float(), cos.float()
+    if x.dim() == 3:
+        s, c = s.unsqueeze(1), c.unsqueeze(1)
+    rot = torch.empty_like(xr)
+    rot[..., ::2] = -xr[..., 1::2]
+    rot[..., 1::2] = xr[..., ::2]
+    out = (xr * c + rot * s).to(orig)
+    return torch.cat([pre, out], dim=-1) if pre is not None else out

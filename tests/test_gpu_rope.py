@@ -111,3 +111,56 @@ def test_single_token_and_empty(dev):
     q, k, v = ops.npu_split_rmsnorm_rope(e, es, es, qw.to(dev), kw.to(dev), 512,
                                          512, 128, 1e-6)
     assert q.shape == (0, 512) and v.shape == (0, 512)
+
+
+# rope_inplace: the shapes of test_rope_inplace.py:96-111 (x [batch, head, 512],
+# rope_dim 64, bf16 sin / cos [batch, 64]) plus 2-D x, fp32 / fp16, fp32
+# sin / cos, odd pair counts (scalar-pair path), strided rows and the C++
+# drop-in.  Tolerance: bf16 rtol 1.6e-2 / atol 1e-2 (fp32: 1e-5); the
+# untouched prefix must be unchanged bit for bit.
+@pytest.mark.parametrize("batch,head", [(1, 8), (4, 8), (8, 8), (1, 1), (4, 1), (8, 1),
+                                        (4096, 16)])
+def test_rope_inplace_reference_cases(dev, batch, head):
+    _check_rope_inplace(dev, (batch, head, 512), 64, torch.bfloat16, torch.bfloat16, batch + head)
+
+
+@pytest.mark.parametrize("shape,rope_dim,dtype,sdtype", [
+    ((33, 256), 64, torch.bfloat16, torch.bfloat16),     # 2-D x
+    ((7, 4, 128), 128, torch.float32, torch.float32),    # whole row rotated
+    ((9, 3, 96), 32, torch.float16, torch.float32),      # fp32 sin / cos
+    ((5, 2, 40), 6, torch.bfloat16, torch.bfloat16),     # 3 pairs: pair path
+])
+def test_rope_inplace_shapes(dev, shape, rope_dim, dtype, sdtype):
+    _check_rope_inplace(dev, shape, rope_dim, dtype, sdtype, 11)
+
+
+def test_rope_inplace_cpp_api_and_strided_rows(dev):
+    from torch_npu_ops_amd import _xk_torch as xt
+    gen = torch.Generator().manual_seed(12)
+    base = torch.randn(64, 640, generator=gen).bfloat16()
+    sin = torch.randn(64, 64, generator=gen).bfloat16()
+    cos = torch.randn(64, 64, generator=gen).bfloat16()
+    xd = base.to(dev)
+    view = xd[:, 64:576]  # rows of 512 at stride 640
+    xt.rope_inplace(view, sin.to(dev), cos.to(dev), 64)
+    torch.cuda.synchronize()
+    ref = orp.rope_inplace_ref(base[:, 64:576], sin, cos, 64)
+    out = xd.cpu()
+    assert torch.equal(out[:, :64], base[:, :64]) and torch.equal(out[:, 576:], base[:, 576:])
+    torch.testing.assert_close(out[:, 64:576].float(), ref.float(), rtol=1.6e-2, atol=1e-2)
+
+
+def _check_rope_inplace(dev, shape, rope_dim, dtype, sdtype, seed):
+    from torch_npu_ops_amd import ops
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(*shape, generator=gen).to(dtype)
+    sin = torch.randn(shape[0], rope_dim, generator=gen).to(sdtype)
+    cos = torch.randn(shape[0], rope_dim, generator=gen).to(sdtype)
+    xd = x.to(dev)
+    ops.rope_inplace(xd, sin.to(dev), cos.to(dev), rope_dim)
+    torch.cuda.synchronize()
+    ref = orp.rope_inplace_ref(x, sin, cos, rope_dim)
+    out = xd.cpu()
+    assert torch.equal(out[..., :-rope_dim], x[..., :-rope_dim])
+    tol = dict(rtol=1e-5, atol=1e-5) if dtype == torch.float32 else dict(rtol=1.6e-2, atol=1e-2)
+    torch.testing.assert_close(out.float(), ref.float(), **tol)

@@ -1,4 +1,5 @@
 """Pins for oracle/rope.py (CPU only)."""
+import pytest
 import torch
 import torch.nn.functional as F
 
@@ -58,3 +59,36 @@ def test_inv_freq_table_values():
     assert inv[0] == 1.0
     torch.testing.assert_close(inv[1].double(), torch.tensor(1e6 ** (-2 / 128),
                                                              dtype=torch.float64))
+
+
+def test_rope_inplace_ref_is_interleaved_complex_rotation():
+    # With cos / sin shared by each pair (cos[2i] = cos[2i+1] = cos t_i), the
+    # interleaved rotation is (x[2i] + i x[2i+1]) * (cos t_i + i sin t_i).
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(5, 3, 40, generator=gen, dtype=torch.float64)
+    t = torch.rand(5, 8, generator=gen, dtype=torch.float64) * 6.0
+    cos = torch.cos(t).repeat_interleave(2, -1)
+    sin = torch.sin(t).repeat_interleave(2, -1)
+    out = orp.rope_inplace_ref(x, sin, cos, 16)
+    assert torch.equal(out[..., :24], x[..., :24])
+    z = torch.complex(x[..., 24::2], x[..., 25::2]) * torch.polar(
+        torch.ones_like(t), t)[:, None, :]
+    torch.testing.assert_close(out[..., 24::2].double(), z.real, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(out[..., 25::2].double(), z.imag, rtol=1e-6, atol=1e-6)
+    # pair norms are preserved, and cos 1 / sin 0 is the identity
+    torch.testing.assert_close(out[..., 24::2] ** 2 + out[..., 25::2] ** 2,
+                               x[..., 24::2] ** 2 + x[..., 25::2] ** 2, rtol=1e-6, atol=1e-6)
+    ident = orp.rope_inplace_ref(x, torch.zeros(5, 16, dtype=torch.float64),
+                                 torch.ones(5, 16, dtype=torch.float64), 16)
+    torch.testing.assert_close(ident, x, rtol=1e-7, atol=1e-7)
+
+
+def test_rope_inplace_ref_uses_each_element_s_own_sin_cos():
+    # The reference rotates with per-element sin / cos (not per pair):
+    # out[1] = x[1] cos[1] + x[0] sin[1].
+    x = torch.tensor([[2.0, 3.0]], dtype=torch.float64)
+    out = orp.rope_inplace_ref(x, torch.tensor([[0.5, 0.25]], dtype=torch.float64),
+                               torch.tensor([[0.1, 0.2]], dtype=torch.float64), 2)
+    # computed in fp32, as the reference does (sin / cos .to(float32))
+    assert out[0].tolist() == pytest.approx([2.0 * 0.1 - 3.0 * 0.5, 3.0 * 0.2 + 2.0 * 0.25],
+                                            rel=1e-6)

@@ -27,12 +27,13 @@ def test_registry_maps_reference_names_to_entry_points(xt):
         "fused_gdn_gating_decode_kernel": "xk_fused_gdn_gating",
         "fused_sigmoid_gating_delta_rule_update_kernel": "xk_gdn_sigmoid_gating_update",
         "fused_qkvzba_split_reshape_cat_gqa_r3_kernel": "xk_fused_qkvzba_split_reshape_cat",
+        "rope_inplace_kernel": "xk_rope_inplace",
     }
     for name, sym in pairs.items():
         assert xt.registry_register(name, "/path/ignored.npubin")
         assert xt.registry_stub(name) == ctypes.cast(getattr(lib, sym), ctypes.c_void_p).value
     # kernels outside the op set are not registered
-    assert not xt.registry_register("rope_inplace_kernel", "")
+    assert not xt.registry_register("_causal_conv1d_fwd_kernel", "")
     assert xt.registry_stub("_causal_conv1d_update_kernel_no_cache_len") == 0
 
 

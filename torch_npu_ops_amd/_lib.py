@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "xk_split_rmsnorm_rope": (
         [P, I64, I64, P, P, I64, P, INT, P, P, P, P, P, P, P, P, INT, I64, I64,
          I64, F32, INT, P], INT),
+    "xk_rope_inplace": ([P, I64, I64, I64, I64, P, P, I64, I64, INT, INT, P], INT),
     "xk_causal_conv1d_update": (
         [P, I64, I64, I64, P, I64, I64, I64, P, I64, I64, P, INT, P, I32, I64,
          P, I64, I64, I64, I64, I64, I64, I64, I64, INT, INT, P], INT),

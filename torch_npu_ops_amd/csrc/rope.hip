@@ -204,10 +204,116 @@ int dispatch_aux(const RopeParams& p, int64_t hd, xk_dtype dt, xk_dtype aux,
   return XK_ERR_UNSUPPORTED;
 }
 
+// ---------------------------------------------------------------------------
+// In-place GPT-J (interleaved) RoPE on the last rope_dim elements of each row
+// (xllm::kernel::npu::rope_inplace; reference rope_ref,
+// triton_npu/triton_src/test_rope_inplace.py:66-94):
+//   out[2i]   = x[2i]   cos[2i]   - x[2i+1] sin[2i]
+//   out[2i+1] = x[2i+1] cos[2i+1] + x[2i]   sin[2i+1]
+// with the sin/cos row of token row / head_num.  One lane per VEC elements
+// (VEC/2 pairs), so each pair is lane-local; the untouched prefix of the row
+// is never read.
+// ---------------------------------------------------------------------------
+template <typename T, typename A, int VEC>
+__global__ void __launch_bounds__(256)
+    rope_inplace_kernel(T* __restrict__ x, const A* __restrict__ sin, const A* __restrict__ cos,
+                        int64_t rows, int head_num, int64_t sx, int64_t ssc, int64_t off,
+                        int lanes_per_row) {
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t row = gid / lanes_per_row;
+  if (row >= rows) return;
+  const int e0 = static_cast<int>(gid - row * lanes_per_row) * VEC;
+  T* xp = x + row * sx + off + e0;
+  const int64_t tok = row / head_num;
+  using VT = Vec<T, VEC>;
+  using VA = Vec<A, VEC>;
+  const VT xv = *reinterpret_cast<const VT*>(xp);
+  const VA sv = *reinterpret_cast<const VA*>(sin + tok * ssc + e0);
+  const VA cv = *reinterpret_cast<const VA*>(cos + tok * ssc + e0);
+  VT ov;
+#pragma unroll
+  for (int u = 0; u < VEC; u += 2) {
+    const float x0 = to_f32(xv.v[u]), x1 = to_f32(xv.v[u + 1]);
+    ov.v[u] = from_f32<T>(x0 * to_f32(cv.v[u]) - x1 * to_f32(sv.v[u]));
+    ov.v[u + 1] = from_f32<T>(x1 * to_f32(cv.v[u + 1]) + x0 * to_f32(sv.v[u + 1]));
+  }
+  *reinterpret_cast<VT*>(xp) = ov;
+}
+
+template <typename T, typename A>
+int launch_rope_inplace(void* x, const void* sin, const void* cos, int64_t rows, int head_num,
+                        int64_t sx, int64_t ssc, int64_t hidden, int64_t rope_dim,
+                        hipStream_t s) {
+  constexpr int kV = 16 / sizeof(T) < 2 ? 2 : 16 / sizeof(T);
+  const int64_t off = hidden - rope_dim;
+  const bool vec = rope_dim % kV == 0 && off % kV == 0 && sx % kV == 0 && ssc % kV == 0 &&
+                   aligned(x, 16) && aligned(sin, kV * sizeof(A)) &&
+                   aligned(cos, kV * sizeof(A));
+  const int v = vec ? kV : 2;
+  const int lanes = static_cast<int>(rope_dim / v);
+  const int64_t total = rows * lanes;
+  const dim3 grid(cdiv(total, 256));
+  T* xp = static_cast<T*>(x);
+  const A* sp = static_cast<const A*>(sin);
+  const A* cp = static_cast<const A*>(cos);
+  if (vec)
+    hipLaunchKernelGGL((rope_inplace_kernel<T, A, kV>), grid, dim3(256), 0, s, xp, sp, cp, rows,
+                       head_num, sx, ssc, off, lanes);
+  else
+    hipLaunchKernelGGL((rope_inplace_kernel<T, A, 2>), grid, dim3(256), 0, s, xp, sp, cp, rows,
+                       head_num, sx, ssc, off, lanes);
+  return launch_status();
+}
+
+template <typename T>
+int rope_inplace_aux(void* x, const void* sin, const void* cos, int64_t rows, int head_num,
+                     int64_t sx, int64_t ssc, int64_t hidden, int64_t rope_dim, xk_dtype dt,
+                     xk_dtype aux, hipStream_t s) {
+  if (aux == dt)
+    return launch_rope_inplace<T, T>(x, sin, cos, rows, head_num, sx, ssc, hidden, rope_dim, s);
+  if (aux == XK_F32)
+    return launch_rope_inplace<T, float>(x, sin, cos, rows, head_num, sx, ssc, hidden,
+                                         rope_dim, s);
+  return XK_ERR_UNSUPPORTED;
+}
+
 }  // namespace
 }  // namespace xk
 
 using namespace xk;
+
+extern "C" int xk_rope_inplace(void* x, int64_t rows, int64_t head_num, int64_t stride_x_row,
+                               int64_t hidden, const void* sin, const void* cos,
+                               int64_t stride_sc_row, int64_t rope_dim, xk_dtype dtype,
+                               xk_dtype sc_dtype, void* stream) {
+  if (rows < 0 || head_num <= 0 || head_num > INT32_MAX || rope_dim <= 0 || rope_dim % 2 ||
+      rope_dim > hidden || stride_x_row < hidden || stride_sc_row < rope_dim ||
+      rope_dim / 2 > INT32_MAX)
+    return XK_ERR_INVALID;
+  if (!is_float_dtype(dtype) || !is_float_dtype(sc_dtype)) return XK_ERR_UNSUPPORTED;
+  if (rows == 0) return XK_OK;
+  if (!x || !sin || !cos) return XK_ERR_INVALID;
+  // Pairs are moved as aligned two-element vectors at the least.
+  if ((hidden - rope_dim) % 2 || stride_x_row % 2 || stride_sc_row % 2 ||
+      !aligned(x, 2 * elem_bytes(dtype)) || !aligned(sin, 2 * elem_bytes(sc_dtype)) ||
+      !aligned(cos, 2 * elem_bytes(sc_dtype)))
+    return XK_ERR_UNSUPPORTED;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int hn = static_cast<int>(head_num);
+  switch (dtype) {
+    case XK_F32:
+      return rope_inplace_aux<float>(x, sin, cos, rows, hn, stride_x_row, stride_sc_row, hidden,
+                                     rope_dim, dtype, sc_dtype, s);
+    case XK_BF16:
+      return rope_inplace_aux<bf16>(x, sin, cos, rows, hn, stride_x_row, stride_sc_row, hidden,
+                                    rope_dim, dtype, sc_dtype, s);
+    case XK_F16:
+      return rope_inplace_aux<f16>(x, sin, cos, rows, hn, stride_x_row, stride_sc_row, hidden,
+                                   rope_dim, dtype, sc_dtype, s);
+    default:
+      return XK_ERR_UNSUPPORTED;
+  }
+}
 
 extern "C" int xk_split_rmsnorm_rope(
     const void* qkv, int64_t stride_qkv_row, int64_t num_tokens,

@@ -69,6 +69,7 @@ class OperationFactory {
   XK_FACTORY(causal_conv1d_update_tiled_v2, CausalConv1dUpdateTiledV2Op,
              "_causal_conv1d_update_kernel_npu_tiled_v2")
   XK_FACTORY(split_rmsnorm_rope, SplitRmsnormRopeOp, "split_rmsnorm_rope_kernel")
+  XK_FACTORY(rope_inplace, RopeInplaceOp, "rope_inplace_kernel")
   XK_FACTORY(fused_qkvzba_split_reshape_gqa_r1, FusedQkvzbaSplitReshapeGqaR1Op,
              "fused_qkvzba_split_reshape_cat_gqa_r1_kernel")
   XK_FACTORY(fused_qkvzba_split_reshape_gqa_r2, FusedQkvzbaSplitReshapeGqaR2Op,

@@ -72,6 +72,7 @@ XK_OPERATION(CausalConv1dUpdateNoCacheNoMtpOp, xk_causal_conv1d_update);
 XK_OPERATION(CausalConv1dUpdateQwenDecodeOp, xk_causal_conv1d_update);
 XK_OPERATION(CausalConv1dUpdateTiledV2Op, xk_causal_conv1d_varlen);
 XK_OPERATION(SplitRmsnormRopeOp, xk_split_rmsnorm_rope);
+XK_OPERATION(RopeInplaceOp, xk_rope_inplace);
 XK_OPERATION(FusedQkvzbaSplitReshapeGqaR1Op, xk_fused_qkvzba_split_reshape_cat);
 XK_OPERATION(FusedQkvzbaSplitReshapeGqaR2Op, xk_fused_qkvzba_split_reshape_cat);
 XK_OPERATION(FusedQkvzbaSplitReshapeGqaR3Op, xk_fused_qkvzba_split_reshape_cat);

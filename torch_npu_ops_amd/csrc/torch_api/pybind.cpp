@@ -35,6 +35,11 @@ PYBIND11_MODULE(_xk_torch, m) {
         "initial_state"_a = OptT(), "inplace_final_state"_a = true, "cu_seqlens"_a = OptT(),
         "ssm_state_indices"_a = OptT(), "num_accepted_tokens"_a = OptT(),
         "use_qk_l2norm_in_kernel"_a = false);
+  m.def("rope_inplace", [](torch::Tensor x, torch::Tensor sin, torch::Tensor cos,
+                           uint32_t rope_dim) {
+    npu::rope_inplace(x, sin, cos, rope_dim);
+    return x;
+  }, "x"_a, "sin"_a, "cos"_a, "rope_dim"_a = 64);
   m.def("npu_fused_gdn_gating", &npu::npu_fused_gdn_gating, "A_log"_a, "a"_a, "b"_a,
         "dt_bias"_a, "beta"_a = 1.0f, "threshold"_a = 20.0f);
   m.def("npu_fused_sigmoid_gating_delta_rule_update",

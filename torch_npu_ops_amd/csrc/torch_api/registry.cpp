@@ -50,6 +50,7 @@ const Entry kKernels[] = {
     {"_causal_conv1d_update_qwen_decode_kernel", reinterpret_cast<void*>(&xk_causal_conv1d_update)},
     {"_causal_conv1d_update_kernel_npu_tiled_v2", reinterpret_cast<void*>(&xk_causal_conv1d_varlen)},
     {"split_rmsnorm_rope_kernel", reinterpret_cast<void*>(&xk_split_rmsnorm_rope)},
+    {"rope_inplace_kernel", reinterpret_cast<void*>(&xk_rope_inplace)},
     {"fused_qkvzba_split_reshape_cat_gqa_r1_kernel",
      reinterpret_cast<void*>(&xk_fused_qkvzba_split_reshape_cat)},
     {"fused_qkvzba_split_reshape_cat_gqa_r2_kernel",

@@ -359,6 +359,31 @@ std::pair<torch::Tensor, torch::Tensor> npu_fused_recurrent_gated_delta_rule(
   return {o, fin};
 }
 
+// triton_npu/torch_api/npu_triton_rope_inplace.cpp:22-64
+void rope_inplace(torch::Tensor& x, torch::Tensor& sin, torch::Tensor& cos, uint32_t rope_dim) {
+  auto org_shape = x.sizes().vec();
+  int64_t bsz = 0, head_num = 0, hidden_size = 0;
+  if (x.dim() == 2) {
+    bsz = x.size(0);
+    head_num = 1;
+    hidden_size = x.size(1);
+  } else if (x.dim() == 3) {
+    bsz = x.size(0);
+    head_num = x.size(1);
+    hidden_size = x.size(2);
+    x = x.view({-1, hidden_size});
+  }
+  TORCH_CHECK(bsz > 0 || x.numel() == 0, "rope_inplace expects a 2-D or 3-D x");
+  TORCH_CHECK(x.stride(-1) == 1, "rope_inplace needs rows with unit column stride");
+  TORCH_CHECK(sin.stride(-1) == 1 && cos.stride(-1) == 1 && sin.stride(0) == cos.stride(0),
+              "sin and cos must share a row stride with unit column stride");
+  check(xk_rope_inplace(x.data_ptr(), bsz * head_num, head_num, x.stride(0), hidden_size,
+                        sin.data_ptr(), cos.data_ptr(), cos.stride(0), rope_dim, xdt(x),
+                        xdt(sin), stream_of(x)),
+        "xk_rope_inplace");
+  if (org_shape.size() == 3) x = x.view(org_shape);
+}
+
 // triton_npu/torch_api/npu_triton_fused_gdn_gating.cpp:33-94
 std::pair<torch::Tensor, torch::Tensor> npu_fused_gdn_gating(torch::Tensor& A_log,
                                                              torch::Tensor& a, torch::Tensor& b,

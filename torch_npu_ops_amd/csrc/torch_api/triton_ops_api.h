@@ -13,8 +13,6 @@
 //    (split_rmsnorm_rope, l2norm);
 //  * the chunked op runs its whole pipeline on the device without reading
 //    cu_seqlens on the host.
-// rope_inplace of the reference header is outside this build's op set and
-// is not declared.
 #pragma once
 
 #include <torch/torch.h>
@@ -48,6 +46,9 @@ torch::Tensor npu_chunk_fwd_o(const torch::Tensor& q, const torch::Tensor& k,
                               const torch::Tensor& v, const torch::Tensor& h,
                               const torch::Tensor& g_cumsum, float scale, int64_t chunk_size,
                               const std::optional<torch::Tensor>& cu_seqlens);
+
+void rope_inplace(torch::Tensor& x, torch::Tensor& sin, torch::Tensor& cos,
+                  uint32_t rope_dim = 64);
 
 std::pair<torch::Tensor, torch::Tensor> npu_fused_gdn_gating(torch::Tensor& A_log,
                                                              torch::Tensor& a, torch::Tensor& b,

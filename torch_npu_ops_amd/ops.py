@@ -195,6 +195,33 @@ def npu_split_rmsnorm_rope(input: torch.Tensor, sin: Optional[torch.Tensor],
     return q, k, v
 
 
+def rope_inplace(x: torch.Tensor, sin: torch.Tensor, cos: torch.Tensor,
+                 rope_dim: int = 64) -> torch.Tensor:
+    """In-place GPT-J (interleaved) RoPE on the last rope_dim elements of
+    each row of x ([bsz, hidden] or [bsz, heads, hidden]); sin / cos are
+    [bsz, >= rope_dim].  Returns x.
+
+    Mirrors rope_inplace (triton_npu/torch_api/npu_triton_rope_inplace.cpp:22-64).
+    """
+    if x.dim() == 2:
+        bsz, heads, hidden = x.size(0), 1, x.size(1)
+        x2 = x
+    elif x.dim() == 3:
+        bsz, heads, hidden = x.shape
+        x2 = x.view(-1, hidden)
+    else:
+        raise ValueError(f"Unsupported dimension: {x.dim()}")
+    if x2.stride(-1) != 1:
+        raise ValueError("rope_inplace needs rows with unit column stride")
+    if sin.stride(-1) != 1 or cos.stride(-1) != 1 or sin.stride(0) != cos.stride(0):
+        raise ValueError("sin and cos must share a row stride with unit column stride")
+    st = lib().xk_rope_inplace(x2.data_ptr(), bsz * heads, heads, x2.stride(0), hidden,
+                               sin.data_ptr(), cos.data_ptr(), cos.stride(0), rope_dim,
+                               xk_dtype(x2), xk_dtype(sin), _stream(x))
+    check(st, "xk_rope_inplace")
+    return x
+
+
 def npu_causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor,
                              weight: torch.Tensor, activation: bool = True,
                              bias: Optional[torch.Tensor] = None,
