@@ -48,7 +48,7 @@ const char* xk_version(void);
 const char* xk_status_string(int status);
 
 /* ------------------------------------------------------------------------
- * a2. Grouped LayerNorm / RMSNorm forward with optional SiLU gate.
+ * Grouped LayerNorm / RMSNorm forward with optional SiLU gate.
  * Replaces xllm::kernel::npu::layer_norm_fwd
  *   (triton_npu/torch_api/triton_ops_api.h:137-145,
  *    npu_triton_layernorm_fwd.cpp:48-332)
@@ -69,7 +69,7 @@ int xk_layer_norm_fwd(const void* x, int64_t stride_x_row, void* y,
                       void* stream);
 
 /* ------------------------------------------------------------------------
- * a3. Gemma RMSNorm: y = x * rsqrt(mean(x^2) + eps) * (1 + gamma), fp32
+ * Gemma RMSNorm: y = x * rsqrt(mean(x^2) + eps) * (1 + gamma), fp32
  * arithmetic, one statistic per row of N = gamma.numel() elements.
  * Replaces npu_ops::npu_gemma_rms_norm (ascendc_npu/ascendc_ops_api.h:24-29,
  * gemma_rms_norm.cpp:28-57).  rstd: fp32 [M] (may be NULL).
@@ -80,7 +80,7 @@ int xk_gemma_rms_norm(const void* x, int64_t stride_x_row, void* y,
                       xk_dtype wdtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * a6a. y = x * rsqrt(sum(x^2) + eps) over the last dim (contiguous rows).
+ * y = x * rsqrt(sum(x^2) + eps) over the last dim (contiguous rows).
  * Replaces npu_l2norm_last_dim (triton_ops_api.h:31, npu_triton_l2norm.cpp).
  */
 int xk_l2norm_last_dim(const void* x, void* y, int64_t rows, int64_t cols,
@@ -88,7 +88,7 @@ int xk_l2norm_last_dim(const void* x, void* y, int64_t rows, int64_t cols,
                        void* stream);
 
 /* ------------------------------------------------------------------------
- * a1. Split a packed [T, q_hidden + 2*kv_hidden] row into q, k, v; per-head
+ * Split a packed [T, q_hidden + 2*kv_hidden] row into q, k, v; per-head
  * RMSNorm of q and k (x * 1/sqrt(mean(x^2)+eps) * w (+ b)) followed by neox
  * rotate-half RoPE over the whole head; v copied through.
  * Replaces xllm::kernel::npu::npu_split_rmsnorm_rope
@@ -133,7 +133,7 @@ int xk_rope_inplace(void* x, int64_t rows, int64_t head_num, int64_t stride_x_ro
                     xk_dtype sc_dtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * a4. Depthwise causal conv1d state update (decode / short MTP windows).
+ * Depthwise causal conv1d state update (decode / short MTP windows).
  * Replaces xllm::kernel::npu::npu_causal_conv1d_update
  *   (triton_npu/torch_api/triton_ops_api.h:147-160,
  *    npu_triton_causal_conv1d_update.cpp:22-138).
@@ -157,7 +157,7 @@ int xk_causal_conv1d_update(
     int64_t state_len, int activation, xk_dtype dtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * a5. Varlen depthwise causal conv1d with conv-state slots (prefill, APC,
+ * Varlen depthwise causal conv1d with conv-state slots (prefill, APC,
  * speculative decoding).
  * Replaces xllm::kernel::npu::npu_causal_conv1d_update_v2
  *   (triton_npu/torch_api/triton_ops_api.h:162-176,
@@ -189,7 +189,7 @@ int xk_causal_conv1d_varlen(
     int32_t pad_slot_id, xk_dtype dtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * a7. Gated delta rule, recurrent form (decode, speculative windows).
+ * Gated delta rule, recurrent form (decode, speculative windows).
  * Replaces xllm::kernel::npu::npu_fused_recurrent_gated_delta_rule
  *   (triton_npu/torch_api/triton_ops_api.h:81-93,
  *    npu_triton_recurrent_gated_delta_rule.cpp:54-247).
@@ -278,7 +278,7 @@ int xk_fused_qkvzba_split_reshape_cat(
     xk_dtype dtype, xk_dtype ba_dtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * a8. One decode step of the gated delta rule fused with the causal conv1d
+ * One decode step of the gated delta rule fused with the causal conv1d
  * update of its mixed q/k/v projection (no single reference function: the
  * composition of npu_causal_conv1d_update, the [q | k | v] channel split of
  * triton_npu/triton_src/test_fused_qkvzba_split_reshape.py:493-500 and
@@ -304,7 +304,7 @@ int xk_gdn_conv_decode(
     int use_qk_l2norm, xk_dtype dtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * a6. Chunked gated delta rule (prefill), chunk size 64.
+ * Chunked gated delta rule (prefill), chunk size 64.
  * Replaces xllm::kernel::npu::npu_chunk_gated_delta_rule
  *   (triton_npu/torch_api/triton_ops_api.h:111-122,
  *    npu_triton_chunk_gated_delta_rule.cpp:556-642) -- the whole pipeline
@@ -331,7 +331,7 @@ int xk_gdn_chunk_fwd(
     size_t workspace_bytes, void* stream);
 
 /*
- * a6b-a6g. The chunked pipeline stage by stage, in the reference's
+ * The chunked pipeline stage by stage, in the reference's
  * intermediate layouts (chunk size 64; chunks restart at every sequence):
  *   g, g_cumsum, beta [T, H]; q, k [T, Hg, K]; v, u, v_new, o [T, H, V];
  *   A, Ai [T, H, 64] (row t: row t - chunk start of the chunk's matrix);

@@ -220,7 +220,7 @@ __device__ __forceinline__ void prep_qk(Smem<K, V>& sm, LoadQK load, bool l2norm
 }
 
 // ---------------------------------------------------------------------------
-// a7: recurrent GDN over varlen sequences.
+// Recurrent GDN over varlen sequences.
 // ---------------------------------------------------------------------------
 struct RecParams {
   const void* q;
@@ -401,7 +401,7 @@ __global__ void __launch_bounds__(256)
 }
 
 // ---------------------------------------------------------------------------
-// a8: decode step fused with the conv1d update.  One block per (batch row,
+// Decode step fused with the conv1d update.  One block per (batch row,
 // qk-head): it owns the conv channels of that q head, that k head and the
 // HV/H v heads of the group, so every conv channel and every state tile is
 // read and written by exactly one block.

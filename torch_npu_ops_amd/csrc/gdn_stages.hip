@@ -1,4 +1,4 @@
-// The chunked gated delta rule as separate stages (a6b..a6g), each with the
+// The chunked gated delta rule as separate stages (cumsum .. output), each with the
 // tensor layout of the reference stage it replaces, for callers that drive
 // the pipeline stage by stage (triton_npu/torch_api/triton_ops_api.h:34-66,
 // 124-135).  The fused xk_gdn_chunk_fwd computes the same result in three
@@ -40,7 +40,7 @@ struct Seq {
 };
 
 // ---------------------------------------------------------------------------
-// a6b: per-chunk cumsum.  One thread per (token, head).
+// Per-chunk cumsum.  One thread per (token, head).
 // ---------------------------------------------------------------------------
 struct CumsumParams : Seq {
   const void* g;
@@ -70,7 +70,7 @@ __global__ void __launch_bounds__(kTh) chunk_cumsum_kernel(CumsumParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// a6c: A = strict_tril(b_i (k_i . k_j) exp(gc_i - gc_j)).  One wave per
+// Scaled K K^T: A = strict_tril(b_i (k_i . k_j) exp(gc_i - gc_j)).  One wave per
 // (chunk, head); the four waves of a block take four heads.
 // ---------------------------------------------------------------------------
 struct KktParams : Seq {
@@ -128,7 +128,7 @@ __global__ void __launch_bounds__(kTh) chunk_kkt_kernel(KktParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// a6d: Ai = (I + A)^-1 per chunk.  One wave per (chunk, head).
+// Triangular solve: Ai = (I + A)^-1 per chunk.  One wave per (chunk, head).
 // ---------------------------------------------------------------------------
 struct TrilParams : Seq {
   const float* A;
@@ -165,7 +165,7 @@ __global__ void __launch_bounds__(kTh) solve_tril_kernel(TrilParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// a6e: u = Ai (v b), w = Ai (k b exp(gc)).  One block per (chunk, head); the
+// WY recompute: u = Ai (v b), w = Ai (k b exp(gc)).  One block per (chunk, head); the
 // right-hand side is staged transposed (token-contiguous) as bf16 hi / lo,
 // wave w produces output columns [w*D/4, (w+1)*D/4) of all 64 rows.
 // ---------------------------------------------------------------------------
@@ -281,7 +281,7 @@ __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// a6f: the state recurrence with per-chunk state snapshots.  One 256-lane
+// The state recurrence with per-chunk state snapshots.  One 256-lane
 // block per (sequence, head, 32-column V tile); the fp32 state lives in
 // registers (wave w: K rows [32w, 32w+32)), its bf16 hi / lo copy in LDS.
 // ---------------------------------------------------------------------------
@@ -443,7 +443,7 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// a6g: o = scale (exp(gc) (q h_c) + tril(q k^T exp(gc_i - gc_j)) v_new).
+// Output: o = scale (exp(gc) (q h_c) + tril(q k^T exp(gc_i - gc_j)) v_new).
 // One block per (chunk, head): h_c and v_new staged transposed in LDS, wave
 // w owns rows [16w, 16w+16) and all V columns.
 // ---------------------------------------------------------------------------

@@ -43,7 +43,7 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 # ---------------------------------------------------------------------------
-# a2 / a3 / a6a: normalisation
+# Normalisation
 # ---------------------------------------------------------------------------
 def layer_norm_fwd(x: torch.Tensor, weight: torch.Tensor,
                    bias: Optional[torch.Tensor], eps: float,
@@ -610,7 +610,7 @@ def npu_chunk_gated_delta_rule(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor
 
 
 # ---------------------------------------------------------------------------
-# a6b-a6g: the chunked pipeline stage by stage
+# The chunked pipeline stage by stage
 # ---------------------------------------------------------------------------
 def _seqs(B: int, T: int, cu_seqlens: Optional[torch.Tensor], dev):
     """(cu tensor on dev, N): the reference's varlen table, or B sequences
