@@ -78,7 +78,7 @@ class LayerNormCase(Case):
     name = "layer_norm_fwd"
     config = ("config 2a: layer_norm_fwd bf16 x[16384,4096], group_size 4096, "
               "affine w~N(1,0.1) b~N(0,0.1), eps 1e-5, outputs y + fp32 mean/rstd")
-    kernel = "ln_tile_kernel"
+    kernel = "ln_tile_kernel<TPG=128,NV=4,z=0>"
     M, N = 16384, 4096
     # x + y (bf16) + mean/rstd (fp32) + w/b (bf16)
     algo_bytes = M * N * 2 * 2 + M * 4 * 2 + N * 2 * 2
@@ -120,7 +120,7 @@ class GemmaCase(Case):
     name = "gemma_rms_norm"
     config = ("config 2b: Gemma RMSNorm bf16 x[16384,4096], gamma~N(1,0.1) "
               "applied as (1+gamma), eps 1e-5, outputs y + fp32 rstd")
-    kernel = "ln_tile_kernel"
+    kernel = "ln_tile_kernel<TPG=128,NV=4,z=0>"
     M, N = 16384, 4096
     algo_bytes = M * N * 2 * 2 + M * 4 + N * 2
 
@@ -161,7 +161,7 @@ class GatedRmsNormCase(Case):
               "x and z bf16 [524288, 128] (16384 tokens x 32 heads), group_size 128, "
               "RMS, gate z*sigmoid(z) after the norm, no bias, eps 1e-6; outputs y + "
               "fp32 rstd")
-    kernel = "ln_tile_kernel"
+    kernel = "ln_tile_kernel<TPG=8,NV=2,z=1>"
     M, N = 524288, 128
     # x, z, y (bf16) + rstd (fp32) + weight
     algo_bytes = M * N * 2 * 3 + M * 4 + N * 2
