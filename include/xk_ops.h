@@ -316,7 +316,8 @@ int xk_gdn_conv_decode(
  *   cu_seqlens[n]..cu_seqlens[n+1] (int32 or int64, device).
  *   initial_state / final_state : fp32 [N, HV, K, V] (NULL = zero / not
  *   written).  use_qk_l2norm applies x / sqrt(sum x^2 + 1e-6) to q and k
- *   first.  K = 128, V a multiple of 32.
+ *   first.  K = 128, V a multiple of 32.  q, k, v 16-byte aligned, o
+ *   8-byte aligned (else XK_ERR_INVALID).
  *   workspace >= xk_gdn_chunk_workspace_bytes(total_tokens, N, HV) bytes,
  *   256-byte aligned (chunk offsets + per-chunk inverse blocks).
  */

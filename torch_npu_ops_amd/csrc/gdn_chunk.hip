@@ -207,13 +207,16 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   __bf16* ail = reinterpret_cast<__bf16*>(rec + kMat);
   __bf16* aqp = reinterpret_cast<__bf16*>(rec + 2 * kMat);
   float* sc = reinterpret_cast<float*>(rec + 3 * kMat);
-  // Lane r stores row r of Ai as hi and lo bf16 rows.
+  // Ai as hi and lo bf16 rows.  Store j covers rows 8j .. 8j + 7, one
+  // contiguous KB (lane: row 8j + lane / 8, columns 8 (lane % 8) .. + 7), so
+  // every store instruction writes whole cache lines.
+  const int sr = lane >> 3, scol = (lane & 7) * 8;
 #pragma unroll
-  for (int j0 = 0; j0 < kC; j0 += 8) {
+  for (int j = 0; j < kC / 8; ++j) {
     bf8_t h, l;
-    split8(&X[lane][j0], h, l);
-    *reinterpret_cast<bf8_t*>(aih + lane * kC + j0) = h;
-    *reinterpret_cast<bf8_t*>(ail + lane * kC + j0) = l;
+    split8(&X[8 * j + sr][scol], h, l);
+    *reinterpret_cast<bf8_t*>(aih + (8 * j + sr) * kC + scol) = h;
+    *reinterpret_cast<bf8_t*>(ail + (8 * j + sr) * kC + scol) = l;
   }
   __builtin_amdgcn_wave_barrier();
 
@@ -238,11 +241,11 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
     }
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
-  for (int j0 = 0; j0 < kC; j0 += 8) {
+  for (int j = 0; j < kC / 8; ++j) {
     bf8_t h;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = static_cast<__bf16>(X[lane][j0 + e]);
-    *reinterpret_cast<bf8_t*>(aqp + lane * kC + j0) = h;
+    for (int e = 0; e < 8; ++e) h[e] = static_cast<__bf16>(X[8 * j + sr][scol + e]);
+    *reinterpret_cast<bf8_t*>(aqp + (8 * j + sr) * kC + scol) = h;
   }
 
   // Per-token factors (lane = token); rows >= L are zero.
@@ -282,8 +285,8 @@ struct __align__(16) P2Smem {
 template <int KK>
 struct EarlyOps {
   bf8_t kA[KK];          // K rows wid*16 + l15 (A operands)
-  bf16 v[2][4];          // v at the lane's C-layout positions (raw: converting
-                         // at load time would stall on the load)
+  bf8_t vA;              // v row wid*16 + l15, tile columns 8*lg .. 8*lg + 7
+                         // (A layout; select_op turns it into C layout)
   f4_t ck, bt;           // factors of rows wid*16 + 4*lg + i
   float egl;             // exp(gc_last)
 };
@@ -295,7 +298,7 @@ template <int KK>
 struct OutOps {          // consumed by the output o = cq (Q S) + Aq Vn
   bf8_t qA[KK];          // Q rows wid*16 + l15
   bf8_t aq[2];           // Aq rows wid*16 + l15
-  f4_t cq;
+  float cq;              // factor of row wid*16 + l15
 };
 
 // Token row of q/k/v for C-layout row `r` (rows >= L read row L-1: finite,
@@ -315,13 +318,9 @@ __device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32
                    hq * K + 8 * lg;
 #pragma unroll
   for (int kk = 0; kk < K / 32; ++kk) ops.kA[kk] = *reinterpret_cast<const bf8_t*>(kp + kk * 32);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const bf16* vp = reinterpret_cast<const bf16*>(p.v) +
-                     tok_row(s, wid * 16 + 4 * lg + i, L) * vrow + vcol0 + l15;
-    ops.v[0][i] = vp[0];
-    ops.v[1][i] = vp[16];
-  }
+  ops.vA = *reinterpret_cast<const bf8_t*>(reinterpret_cast<const bf16*>(p.v) +
+                                           tok_row(s, wid * 16 + l15, L) * vrow + vcol0 +
+                                           8 * lg);
   const float* sc = reinterpret_cast<const float*>(rec_at(p, cidx, hv) + 3 * kMat);
   const int r4 = wid * 16 + 4 * lg;
   ops.ck = *reinterpret_cast<const f4_t*>(sc + 1 * kC + r4);
@@ -362,18 +361,27 @@ __device__ __forceinline__ void load_out(const ChunkParams& p, OutOps<K / 32>& o
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)
     ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + (wid * 16 + l15) * kC + kk * 32 + 8 * lg);
-  ops.cq = *reinterpret_cast<const f4_t*>(sc + 0 * kC + wid * 16 + 4 * lg);
+  ops.cq = sc[0 * kC + wid * 16 + l15];
 }
 
-// K rows of the lane's A operands written transposed: kt[k][token].
+// K rows of the lane's A operands written transposed, kt[k][token]: the
+// select_op MFMAs hand each lane 4 consecutive tokens of one key column,
+// stored as one 8-byte vector (bank-conflict-free at the kLt row stride).
 template <int K>
-__device__ __forceinline__ void store_kt(__bf16 (*kt)[kLt], const bf8_t (&kA)[K / 32]) {
+__device__ __forceinline__ void store_kt(__bf16 (*kt)[kLt], const bf8_t (&kA)[K / 32],
+                                         const bf8_t (&sel)[2]) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int row = wid * 16 + (lane & 15), lg = lane >> 4;
+  const int l15 = lane & 15, lg = lane >> 4;
 #pragma unroll
   for (int kk = 0; kk < K / 32; ++kk)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) kt[kk * 32 + 8 * lg + e][row] = kA[kk][e];
+    for (int h = 0; h < 2; ++h) {
+      const f4_t c = mfma16(kA[kk], sel[h], f4_t{0.f, 0.f, 0.f, 0.f});
+      Vec<__bf16, 4> b;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(c[i]);
+      *reinterpret_cast<Vec<__bf16, 4>*>(&kt[kk * 32 + 16 * h + l15][wid * 16 + 4 * lg]) = b;
+    }
 }
 
 template <int K, typename T>
@@ -434,15 +442,23 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   publish_state();
   const uint32_t vrow = static_cast<uint32_t>(p.HV) * V;  // v / o token stride
   const int vcol0 = hv * V + v0;
+  const bf8_t sel[2] = {select_op(0), select_op(1)};
   EarlyOps<KK> opsA, opsB;
   InvOps inv;
   OutOps<KK> outo;
   if (nch > 0) {
     const int L0 = static_cast<int>(min<int64_t>(kC, eos - bos));
     load_early<K>(p, opsA, bos, L0, cidx0, hv, hq, vrow, vcol0);
+    // Keep the early group ahead of the others, in loop order: the loop's
+    // wait counts are fixed by the shortest distance (in memory operations)
+    // between a load and its first use over every path, this one included,
+    // and an early load scheduled last here would make every chunk wait for
+    // the previous chunk's most recent loads.
+    __builtin_amdgcn_sched_barrier(0);
     load_inv(p, inv, cidx0, hv);
+    __builtin_amdgcn_sched_barrier(0);
     load_out<K>(p, outo, bos, L0, cidx0, hv, hq);
-    store_kt<K>(sm.kt[0], opsA.kA);
+    store_kt<K>(sm.kt[0], opsA.kA, sel);
   }
   __syncthreads();
 
@@ -476,9 +492,10 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj) {
       Vec<__bf16, 4> h, l;
+      const f4_t vc = mfma16(cur.vA, sel[nj], f4_t{0.f, 0.f, 0.f, 0.f});
       f4_t rv;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rv[i] = cur.bt[i] * to_f32(cur.v[nj][i]) - cur.ck[i] * ks[nj][i];
+      for (int i = 0; i < 4; ++i) rv[i] = cur.bt[i] * vc[i] - cur.ck[i] * ks[nj][i];
       split4(rv, h, l);
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = h;
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = l;
@@ -513,8 +530,12 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = l;
     }
     load_inv(p, inv, cidx0 + cn, hv);  // this chunk is done with `inv`
-    // Q S with the hi part of S.  It must read sb before barrier 2: after it,
-    // a wave that is ahead may already publish the next state into sb.
+    // (Q S)^T = S^T Q^T with the hi part of S: the output is produced
+    // transposed (lane: token wid*16 + l15, columns 4*lg .. 4*lg + 3), so
+    // each lane stores one 8-byte vector per column tile.  The S^T A operand
+    // is the same sb read as S's B operand, and Q^T's B operand is Q's A
+    // operand.  It must read sb before barrier 2: after it, a wave that is
+    // ahead may already publish the next state into sb.
     f4_t qs[2];
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj) {
@@ -522,30 +543,32 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
-        qs[nj] = mfma16(outo.qA[kk], sh, qs[nj]);
+        qs[nj] = mfma16(sh, outo.qA[kk], qs[nj]);
       }
     }
     __syncthreads();  // (2) vt, dt complete; rt and sb reads done
 
-    // o = cq (Q S) + Aq Vn.
+    // o^T = cq (Q S)^T + Vn^T Aq^T (Vn^T's A operand is the vt read that
+    // was Vn's B operand; Aq^T's B operand is Aq's A operand).
+    {
+      const int row = wid * 16 + l15;
+      T* orow = row < L ? reinterpret_cast<T*>(p.o) + static_cast<uint64_t>(s + row) * vrow + vcol0
+                        : reinterpret_cast<T*>(p.dump) + row * kBV;
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj) {
-      f4_t acc;
+      for (int nj = 0; nj < 2; ++nj) {
+        f4_t acc;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = outo.cq[i] * qs[nj][i];
+        for (int i = 0; i < 4; ++i) acc[i] = outo.cq * qs[nj][i];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        if (kk * 32 > wid * 16 + 15) continue;  // Aq columns beyond the diagonal
-        const bf8_t vb = *reinterpret_cast<const bf8_t*>(&sm.vt[nj * 16 + l15][kk * 32 + 8 * lg]);
-        acc = mfma16(outo.aq[kk], vb, acc);
-      }
+        for (int kk = 0; kk < 2; ++kk) {
+          if (kk * 32 > wid * 16 + 15) continue;  // Aq columns beyond the diagonal
+          const bf8_t vb = *reinterpret_cast<const bf8_t*>(&sm.vt[nj * 16 + l15][kk * 32 + 8 * lg]);
+          acc = mfma16(vb, outo.aq[kk], acc);
+        }
+        Vec<T, 4> ov;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = wid * 16 + 4 * lg + i;
-        T* dst = row < L ? reinterpret_cast<T*>(p.o) + static_cast<uint64_t>(s + row) * vrow +
-                               vcol0 + nj * 16 + l15
-                         : reinterpret_cast<T*>(p.dump) + row * kBV + nj * 16 + l15;
-        *dst = from_f32<T>(acc[i]);
+        for (int i = 0; i < 4; ++i) ov.v[i] = from_f32<T>(acc[i]);
+        *reinterpret_cast<Vec<T, 4>*>(orow + nj * 16 + 4 * lg) = ov;
       }
     }
     load_out<K>(p, outo, sn, Ln, cidx0 + cn, hv, hq);  // this chunk is done with `outo`
@@ -576,7 +599,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       }
     }
     publish_state();
-    store_kt<K>(sm.kt[(ci + 1) & 1], nxt.kA);
+    store_kt<K>(sm.kt[(ci + 1) & 1], nxt.kA, sel);
     __syncthreads();  // (3) state copy, next keys complete; vt / dt / kt reads done
   };
   // Unrolled by two so the operand buffers swap roles without copies.
@@ -657,7 +680,8 @@ extern "C" int xk_gdn_chunk_fwd(
   // Token indices travel as int32 in the chunk table.
   if (total_tokens > INT32_MAX - kC) return XK_ERR_UNSUPPORTED;
   if (!q || !k || !v || !g || !beta || !o || !cu_seqlens) return XK_ERR_INVALID;
-  if (!aligned(q, 16) || !aligned(k, 16)) return XK_ERR_INVALID;
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 8))
+    return XK_ERR_INVALID;
   const int64_t need = xk_gdn_chunk_workspace_bytes(total_tokens, N, HV);
   if (!workspace || static_cast<int64_t>(workspace_bytes) < need) return XK_ERR_WORKSPACE;
   if (!aligned(workspace, 256)) return XK_ERR_WORKSPACE;

@@ -80,6 +80,21 @@ __device__ __forceinline__ void split8(const float* p, bf8_t& h, bf8_t& l) {
   }
 }
 
+// B operand that selects columns 16h .. 16h + 15 of a 32-wide A operand:
+// mfma16(a, select_op(h), 0) is that 16 x 16 block of A in C layout, so a
+// lane that held 8 consecutive columns of one row (A layout) receives 4
+// consecutive rows of one column -- a register transpose.  The products
+// with 1 and the sums with 0 are exact.
+__device__ __forceinline__ bf8_t select_op(int h) {
+  const int lane = threadIdx.x & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  bf8_t b;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    b[e] = static_cast<__bf16>(8 * lg + e == l15 + 16 * h ? 1.0f : 0.0f);
+  return b;
+}
+
 // (ah + al)(bh + bl) without the lo*lo term.
 __device__ __forceinline__ f4_t mfma_split3(const bf8_t& ah, const bf8_t& al, const bf8_t& bh,
                                             const bf8_t& bl, f4_t c) {
@@ -133,57 +148,75 @@ template <class P>
 __global__ void __launch_bounds__(256) chunk_offsets_kernel(P p, int32_t* order, int2* table,
                                                             int64_t ntab) {
   constexpr int kT = 256;
-  __shared__ int32_t part[kT];
+  __shared__ int32_t part[kT / kWave];
+  // Up to kSortMaxSeqs sequences, cu_seqlens and the offsets are also kept
+  // in LDS, so the table and ranking passes make no dependent global reads.
+  __shared__ int64_t scu[kSortMaxSeqs + 1];
+  __shared__ int32_t soff[kSortMaxSeqs + 1];
   const int tid = threadIdx.x;
+  const bool small = p.N <= kSortMaxSeqs;
+  if (small)
+    for (int64_t i = tid; i <= p.N; i += kT) scu[i] = cu_at(p, i);
+  __syncthreads();
+  auto cuv = [&](int64_t i) { return small ? scu[i] : cu_at(p, i); };
+  auto nchunks = [&](int64_t n) {
+    const int64_t len = cuv(n + 1) - cuv(n);
+    return static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+  };
   const int64_t per = (p.N + kT - 1) / kT;
   const int64_t b0 = tid * per, b1 = min(p.N, b0 + per);
   int32_t s = 0;
-  for (int64_t n = b0; n < b1; ++n) s += seq_chunks(p, n);
-  part[tid] = s;
-  __syncthreads();
-  if (tid == 0) {
-    int32_t acc = 0;
-    for (int i = 0; i < kT; ++i) {
-      const int32_t v = part[i];
-      part[i] = acc;
-      acc += v;
-    }
+  for (int64_t n = b0; n < b1; ++n) s += nchunks(n);
+  // Exclusive scan of the per-thread counts: wave64 shuffle scans, then the
+  // four wave totals through LDS.
+  const int lane = tid & (kWave - 1), wid = tid / kWave;
+  int32_t incl = s;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int32_t t = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += t;
   }
+  if (lane == kWave - 1) part[wid] = incl;
   __syncthreads();
-  int32_t acc = part[tid];
+  int32_t acc = incl - s;
+  for (int w = 0; w < wid; ++w) acc += part[w];
   for (int64_t n = b0; n < b1; ++n) {
     p.chunk_off[n] = acc;
-    acc += seq_chunks(p, n);
+    if (small) soff[n] = acc;
+    acc += nchunks(n);
   }
-  if (tid == kT - 1) p.chunk_off[p.N] = acc;
+  if (tid == kT - 1) {
+    p.chunk_off[p.N] = acc;
+    if (small) soff[p.N] = acc;
+  }
+  __syncthreads();  // offsets complete and visible to the block
+  auto offv = [&](int64_t i) { return small ? soff[i] : p.chunk_off[i]; };
   if (table) {
-    __syncthreads();  // chunk_off complete and visible to the block
-    const int64_t total = p.chunk_off[p.N];
+    const int64_t total = offv(p.N);
     for (int64_t c = tid; c < ntab; c += kT) {
       int2 e = make_int2(0, 0);
       if (c < total) {
-        int64_t lo = 0, hi = p.N;  // chunk_off[lo] <= c < chunk_off[hi]
+        int64_t lo = 0, hi = p.N;  // off[lo] <= c < off[hi]
         while (hi - lo > 1) {
           const int64_t mid = (lo + hi) >> 1;
-          if (p.chunk_off[mid] <= c) lo = mid; else hi = mid;
+          if (offv(mid) <= c) lo = mid; else hi = mid;
         }
-        const int64_t s0 = cu_at(p, lo) + (c - p.chunk_off[lo]) * kC;
+        const int64_t s0 = cuv(lo) + (c - offv(lo)) * kC;
         e = make_int2(static_cast<int>(s0),
-                      static_cast<int>(min<int64_t>(kC, cu_at(p, lo + 1) - s0)));
+                      static_cast<int>(min<int64_t>(kC, cuv(lo + 1) - s0)));
       }
       table[c] = e;
     }
   }
   if (!order) return;
   // Ranks are a permutation of [0, N): distinct (chunks, index) keys.
-  const bool sort = p.N <= kSortMaxSeqs;
   for (int64_t n = tid; n < p.N; n += kT) {
     int64_t rank = n;
-    if (sort) {
-      const int32_t cn = seq_chunks(p, n);
+    if (small) {
+      const int32_t cn = nchunks(n);
       rank = 0;
       for (int64_t m = 0; m < p.N; ++m) {
-        const int32_t cm = seq_chunks(p, m);
+        const int32_t cm = nchunks(m);
         rank += (cm > cn) || (cm == cn && m < n);
       }
     }
