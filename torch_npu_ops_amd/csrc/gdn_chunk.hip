@@ -46,7 +46,7 @@ namespace {
 
 using namespace gdn;
 
-constexpr int kBV = 32;   // V columns per P2 block
+constexpr int kBVMax = 64;  // most V columns per P2 block (32 or 64)
 constexpr int kTh = 256;  // threads per block
 // Per-(chunk, head) record: ai_hi, ai_lo, aq (bf16 [64][64] each), then the
 // per-token factors (fp32 [5][64]: cq, ck, b, ed, exp(gc_last)).
@@ -57,7 +57,7 @@ static_assert(kRec % 256 == 0, "records stay 256-byte aligned");
 // so that every store in the chunk loop is unconditional: gfx9 counts loads
 // and stores in one in-order counter, and a store that only some paths
 // issue makes the compiler wait for every outstanding prefetch.
-constexpr int kDump = kC * kBV * 2;
+constexpr int kDump = kC * kBVMax * 2;
 
 struct ChunkParams {
   const void* q;  // [T, H, K]
@@ -267,13 +267,13 @@ constexpr int kLt = kC + 8;  // bf16 LDS row stride (144 B: 16-byte aligned)
 // The fp32 state tile itself lives in registers (each wave owns K/4 of its
 // rows, in MFMA C layout); LDS holds its bf16 hi / lo copy, the B operand of
 // K S, refreshed once per chunk.
-template <int K>
+template <int K, int BV>
 struct __align__(16) P2Smem {
-  __bf16 sb[2][kBV][K + 8];   // state hi / lo, transposed: sb[h][v][k]
+  __bf16 sb[2][BV][K + 8];    // state hi / lo, transposed: sb[h][v][k]
   __bf16 kt[2][K][kLt];       // chunk keys transposed, double-buffered
-  __bf16 rt[2][kBV][kLt];     // R transposed, hi / lo
-  __bf16 vt[kBV][kLt];        // Vn transposed (bf16, for the output)
-  __bf16 dt[2][kBV][kLt];     // (ed * Vn) transposed, hi / lo
+  __bf16 rt[2][BV][kLt];      // R transposed, hi / lo
+  __bf16 vt[BV][kLt];         // Vn transposed (bf16, for the output)
+  __bf16 dt[2][BV][kLt];      // (ed * Vn) transposed, hi / lo
 };
 
 // Operands one lane reads from global memory for one chunk, in three
@@ -282,10 +282,10 @@ struct __align__(16) P2Smem {
 // the next chunk's operands right after their last use in the current chunk
 // (so each load has most of a chunk to land) -- this keeps two waves per
 // SIMD.
-template <int KK>
+template <int KK, int NV32>
 struct EarlyOps {
   bf8_t kA[KK];          // K rows wid*16 + l15 (A operands)
-  bf8_t vA;              // v row wid*16 + l15, tile columns 8*lg .. 8*lg + 7
+  bf8_t vA[NV32];        // v row wid*16 + l15, tile columns 32j + 8*lg .. + 7
                          // (A layout; select_op turns it into C layout)
   f4_t ck, bt;           // factors of rows wid*16 + 4*lg + i
   float egl;             // exp(gc_last)
@@ -307,8 +307,8 @@ __device__ __forceinline__ uint64_t tok_row(int64_t s, int r, int L) {
   return static_cast<uint64_t>(s + min(r, L - 1));
 }
 
-template <int K>
-__device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32>& ops,
+template <int K, int BV>
+__device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32, BV / 32>& ops,
                                            int64_t s, int L, int64_t cidx, int hv, int hq,
                                            uint32_t vrow, int vcol0) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -318,9 +318,10 @@ __device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32
                    hq * K + 8 * lg;
 #pragma unroll
   for (int kk = 0; kk < K / 32; ++kk) ops.kA[kk] = *reinterpret_cast<const bf8_t*>(kp + kk * 32);
-  ops.vA = *reinterpret_cast<const bf8_t*>(reinterpret_cast<const bf16*>(p.v) +
-                                           tok_row(s, wid * 16 + l15, L) * vrow + vcol0 +
-                                           8 * lg);
+  const bf16* vp = reinterpret_cast<const bf16*>(p.v) + tok_row(s, wid * 16 + l15, L) * vrow +
+                   vcol0 + 8 * lg;
+#pragma unroll
+  for (int j = 0; j < BV / 32; ++j) ops.vA[j] = *reinterpret_cast<const bf8_t*>(vp + 32 * j);
   const float* sc = reinterpret_cast<const float*>(rec_at(p, cidx, hv) + 3 * kMat);
   const int r4 = wid * 16 + 4 * lg;
   ops.ck = *reinterpret_cast<const f4_t*>(sc + 1 * kC + r4);
@@ -384,12 +385,16 @@ __device__ __forceinline__ void store_kt(__bf16 (*kt)[kLt], const bf8_t (&kA)[K 
     }
 }
 
-template <int K, typename T>
-// Two waves per SIMD (<= 256 registers per lane): two blocks share a CU.
-__global__ void __launch_bounds__(kTh) __attribute__((amdgpu_waves_per_eu(2)))
+// BV = 32: two waves per SIMD (<= 256 registers per lane), two blocks share
+// a CU.  BV = 64: one wave per SIMD with up to 512 registers; every loaded
+// K / Q / Ai / Aq operand serves twice the columns.
+template <int K, typename T, int BV>
+__global__ void __launch_bounds__(kTh) __attribute__((amdgpu_waves_per_eu(BV == 32 ? 2 : 1)))
 gdn_chunk_state_kernel(ChunkParams p, int nvt) {
-  __shared__ P2Smem<K> sm;
+  static_assert(BV == 32 || BV == 64, "V tile of 32 or 64 columns");
+  __shared__ P2Smem<K, BV> sm;
   constexpr int KK = K / 32;
+  constexpr int NJ = BV / 16;  // 16-column tiles per block
   const int tid = threadIdx.x;
   const int wid = tid >> 6;
   const int lane = tid & 63;
@@ -406,8 +411,8 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   const int64_t n = p.seq_order[item / p.HV];
   const int hv = static_cast<int>(item % p.HV);
   const int hq = hv / (p.HV / p.H);
-  const int V = nvt * kBV;
-  const int v0 = vt * kBV;
+  const int V = nvt * BV;
+  const int v0 = vt * BV;
   const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
   const int64_t cidx0 = p.chunk_off[n];
   // Chunks of this sequence; the NTmax bound keeps a malformed cu_seqlens
@@ -416,11 +421,11 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 
   // State rows (k) wid*(K/4) + m2*16 + 4*lg + i, columns nj*16 + l15.
   constexpr int M2 = K / 64;
-  f4_t sreg[M2][2];
+  f4_t sreg[M2][NJ];
 #pragma unroll
   for (int m2 = 0; m2 < M2; ++m2)
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj)
+    for (int nj = 0; nj < NJ; ++nj)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
@@ -431,7 +436,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 #pragma unroll
     for (int m2 = 0; m2 < M2; ++m2)
 #pragma unroll
-      for (int nj = 0; nj < 2; ++nj) {
+      for (int nj = 0; nj < NJ; ++nj) {
         Vec<__bf16, 4> h, l;
         split4(sreg[m2][nj], h, l);
         const int k0 = wid * (K / 4) + m2 * 16 + 4 * lg;
@@ -443,12 +448,12 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   const uint32_t vrow = static_cast<uint32_t>(p.HV) * V;  // v / o token stride
   const int vcol0 = hv * V + v0;
   const bf8_t sel[2] = {select_op(0), select_op(1)};
-  EarlyOps<KK> opsA, opsB;
+  EarlyOps<KK, BV / 32> opsA, opsB;
   InvOps inv;
   OutOps<KK> outo;
   if (nch > 0) {
     const int L0 = static_cast<int>(min<int64_t>(kC, eos - bos));
-    load_early<K>(p, opsA, bos, L0, cidx0, hv, hq, vrow, vcol0);
+    load_early<K, BV>(p, opsA, bos, L0, cidx0, hv, hq, vrow, vcol0);
     // Keep the early group ahead of the others, in loop order: the loop's
     // wait counts are fixed by the shortest distance (in memory operations)
     // between a load and its first use over every path, this one included,
@@ -467,22 +472,22 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   // right after their last use here.  The last chunk "prefetches" itself
   // again (unused), so that every memory operation of the loop is
   // unconditional.
-  auto step = [&](const EarlyOps<KK>& cur, EarlyOps<KK>& nxt, int64_t ci) {
+  auto step = [&](const EarlyOps<KK, BV / 32>& cur, EarlyOps<KK, BV / 32>& nxt, int64_t ci) {
     const int64_t s = bos + ci * kC;
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
     const int64_t cn = min(ci + 1, nch - 1);
     const int64_t sn = bos + cn * kC;
     const int Ln = static_cast<int>(min<int64_t>(kC, eos - sn));
-    load_early<K>(p, nxt, sn, Ln, cidx0 + cn, hv, hq, vrow, vcol0);
+    load_early<K, BV>(p, nxt, sn, Ln, cidx0 + cn, hv, hq, vrow, vcol0);
 
     // KS = K S (hi/lo S): rows wid*16.., columns nj*16..
-    f4_t ks[2];
+    f4_t ks[NJ];
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj) ks[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
+    for (int nj = 0; nj < NJ; ++nj) ks[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
-      for (int nj = 0; nj < 2; ++nj) {
+      for (int nj = 0; nj < NJ; ++nj) {
         const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
         const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][kk * 32 + 8 * lg]);
         ks[nj] = mfma16(cur.kA[kk], sh, ks[nj]);
@@ -490,9 +495,9 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       }
     // R = b v - ck KS  ->  rt (transposed, hi / lo); padded rows are 0.
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj) {
+    for (int nj = 0; nj < NJ; ++nj) {
       Vec<__bf16, 4> h, l;
-      const f4_t vc = mfma16(cur.vA, sel[nj], f4_t{0.f, 0.f, 0.f, 0.f});
+      const f4_t vc = mfma16(cur.vA[nj >> 1], sel[nj & 1], f4_t{0.f, 0.f, 0.f, 0.f});
       f4_t rv;
 #pragma unroll
       for (int i = 0; i < 4; ++i) rv[i] = cur.bt[i] * vc[i] - cur.ck[i] * ks[nj][i];
@@ -503,9 +508,9 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     __syncthreads();  // (1) rt complete
 
     // Vn = Ai R.
-    f4_t vn[2];
+    f4_t vn[NJ];
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj) {
+    for (int nj = 0; nj < NJ; ++nj) {
       vn[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
@@ -516,7 +521,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     }
     // Vn -> vt (bf16), ed * Vn -> dt (hi / lo).
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj) {
+    for (int nj = 0; nj < NJ; ++nj) {
       Vec<__bf16, 4> b, h, l;
       f4_t d;
 #pragma unroll
@@ -536,9 +541,9 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     // is the same sb read as S's B operand, and Q^T's B operand is Q's A
     // operand.  It must read sb before barrier 2: after it, a wave that is
     // ahead may already publish the next state into sb.
-    f4_t qs[2];
+    f4_t qs[NJ];
 #pragma unroll
-    for (int nj = 0; nj < 2; ++nj) {
+    for (int nj = 0; nj < NJ; ++nj) {
       qs[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
@@ -553,9 +558,9 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     {
       const int row = wid * 16 + l15;
       T* orow = row < L ? reinterpret_cast<T*>(p.o) + static_cast<uint64_t>(s + row) * vrow + vcol0
-                        : reinterpret_cast<T*>(p.dump) + row * kBV;
+                        : reinterpret_cast<T*>(p.dump) + row * BV;
 #pragma unroll
-      for (int nj = 0; nj < 2; ++nj) {
+      for (int nj = 0; nj < NJ; ++nj) {
         f4_t acc;
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] = outo.cq * qs[nj][i];
@@ -584,7 +589,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       for (int kk = 0; kk < 2; ++kk)
         ka[kk] = *reinterpret_cast<const bf8_t*>(&kt[mi * 16 + l15][kk * 32 + 8 * lg]);
 #pragma unroll
-      for (int nj = 0; nj < 2; ++nj) {
+      for (int nj = 0; nj < NJ; ++nj) {
         f4_t acc = sreg[m2][nj];
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[i] *= cur.egl;
@@ -611,7 +616,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 #pragma unroll
     for (int m2 = 0; m2 < M2; ++m2)
 #pragma unroll
-      for (int nj = 0; nj < 2; ++nj)
+      for (int nj = 0; nj < NJ; ++nj)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
@@ -630,10 +635,11 @@ int launch_chunk(const ChunkParams& p, int64_t V, hipStream_t s) {
                      dim3(kTh), 0, s, p);
   st = launch_status();
   if (st) return st;
-  const int nvt = static_cast<int>(V / kBV);
+  constexpr int BV = 32;
+  const int nvt = static_cast<int>(V / BV);
   const int64_t items = p.N * p.HV;
   const int64_t blocks = cdiv(items, 8) * 8 * nvt;
-  hipLaunchKernelGGL((gdn_chunk_state_kernel<K, bf16>), dim3(blocks), dim3(kTh), 0, s, p, nvt);
+  hipLaunchKernelGGL((gdn_chunk_state_kernel<K, bf16, BV>), dim3(blocks), dim3(kTh), 0, s, p, nvt);
   return launch_status();
 }
 
@@ -675,7 +681,7 @@ extern "C" int xk_gdn_chunk_fwd(
   if (g_dtype != XK_F32 && g_dtype != XK_BF16) return XK_ERR_UNSUPPORTED;
   if (beta_dtype != XK_F32 && beta_dtype != XK_BF16) return XK_ERR_UNSUPPORTED;
   if (cu_dtype != XK_I32 && cu_dtype != XK_I64) return XK_ERR_UNSUPPORTED;
-  if (K != 128 || V % kBV != 0 || V <= 0) return XK_ERR_UNSUPPORTED;
+  if (K != 128 || V % 32 != 0 || V <= 0) return XK_ERR_UNSUPPORTED;
   if (N == 0 || total_tokens == 0) return XK_OK;
   // Token indices travel as int32 in the chunk table.
   if (total_tokens > INT32_MAX - kC) return XK_ERR_UNSUPPORTED;
