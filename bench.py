@@ -11,7 +11,9 @@ smaller ops (configs 1 and 3b, and the gating / in-place RoPE lines), whose
 kernels are not much longer than a Python launch, are captured in one HIP
 graph that is replayed.  Inputs
 rotate over several buffer sets whose total exceeds the 256 MB Infinity
-Cache, so timings see HBM.
+Cache, so timings see HBM.  Before its W warm-up calls every op runs
+untimed for SETTLE_S seconds, so that the GPU clocks have settled at their
+sustained-load level when the timed calls start.
 
 Rank 0 prints ONE JSON line:
   value        achieved GB/s of the headline op (algorithmic bytes / time)
@@ -746,9 +748,29 @@ HEADLINE = "layer_norm_fwd"
 # ---------------------------------------------------------------------------
 # Timing
 # ---------------------------------------------------------------------------
+# Untimed wall time each op runs before its warm-up calls.  The GPU raises
+# its clocks only after some tens of milliseconds of sustained load: on
+# MI355X a 47 us layer_norm_fwd call measures ~51 us until about 20 ms of
+# back-to-back calls have run, and ~46.7 us from then on.  The settle phase
+# makes every op's number the steady-state rate a serving loop sees.
+SETTLE_S = 0.1
+
+
+def _settle(fn):
+    """Call fn() back to back until SETTLE_S of wall time has passed (the
+    GPU stays busy: calls are queued in batches and synchronised only
+    between batches)."""
+    end = time.perf_counter() + SETTLE_S
+    while time.perf_counter() < end:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
 def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
     """Mean per-call time (ms) of `steps` back-to-back calls, median of
-    three timed repetitions."""
+    three timed repetitions, after a clock-settle phase and `warmup`
+    untimed calls."""
     per_set = max(case.algo_bytes, 1)
     nsets = max(2, min(MAX_SETS, -(-ROTATE_BYTES // per_set)))
     runs = case.sets(dev, nsets)
@@ -762,6 +784,12 @@ def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
     if eager:
+        ctr = [0]
+
+        def one():
+            runs[ctr[0] % nsets]()
+            ctr[0] += 1
+        _settle(one)
         reps = []
         for _ in range(3):
             t0.record()
@@ -778,6 +806,7 @@ def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
                 runs[i % nsets]()
         graph.replay()
         torch.cuda.synchronize()
+        _settle(graph.replay)
         reps = []
         for _ in range(3):
             t0.record()
@@ -926,6 +955,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": SETTLE_S,
         "ms_per_step": round(head["us_per_call"] / 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
