@@ -738,10 +738,106 @@ class GdnChunkCase(Case):
                 "chunked form of the reference golden", self.HV / len(heads))
 
 
+class GdnChunkStagedCase(GdnChunkCase):
+    """Config 4 through the six stage entry points in the reference's order
+    (npu_triton_chunk_gated_delta_rule.cpp:556-642): cumsum, scaled K K^T,
+    solve_tril (bf16 Ai), w/u, the state recurrence (bf16 h snapshots and
+    v_new) and the output, with every intermediate in HBM."""
+    name = "gdn_chunk_staged"
+    config = ("config 4 through the stage-by-stage API (chunk_local_cumsum, "
+              "scaled_dot_kkt, solve_tril, recompute_w_u, fwd_h, fwd_o), the "
+              "reference's intermediates (A, Ai, w, u, h, v_new) kept in HBM")
+    kernel = "chunk_fwd_h_kernel"
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        cu = self.cu.to(dev)
+        lens = (self.cu[1:] - self.cu[:-1]).tolist()
+        nt = sum(-(-int(x) // 64) for x in lens)
+        wsb = lib.xk_gdn_stage_workspace_bytes(self.NSEQ)
+        T, H, HV, K, V = self.T, self.H, self.HV, self.K, self.V
+        bf, f32 = torch.bfloat16, torch.float32
+        out = []
+        for _ in range(n):
+            q, k, v = self.q.to(dev), self.k.to(dev), self.v.to(dev)
+            g, beta, h0 = self.g.to(dev), self.beta.to(dev), self.h0.to(dev)
+            b = dict(
+                gc=torch.empty(T, HV, dtype=f32, device=dev),
+                A=torch.empty(T, HV, 64, dtype=f32, device=dev),
+                Ai=torch.empty(T, HV, 64, dtype=bf, device=dev),
+                w=torch.empty(T, HV, K, dtype=bf, device=dev),
+                u=torch.empty(T, HV, V, dtype=bf, device=dev),
+                h=torch.empty(nt, HV, K, V, dtype=bf, device=dev),
+                vn=torch.empty(T, HV, V, dtype=bf, device=dev),
+                ht=torch.empty_like(h0), o=torch.empty_like(v),
+                ws=torch.empty(wsb, dtype=torch.uint8, device=dev))
+
+            def run(q=q, k=k, v=v, g=g, beta=beta, h0=h0, b=b):
+                st = _cur_stream()
+                I32, BF, F32 = _lib.XK_I32, _lib.XK_BF16, _lib.XK_F32
+                ws, wsn = b["ws"].data_ptr(), wsb
+                _ok(lib.xk_chunk_local_cumsum(g.data_ptr(), F32, b["gc"].data_ptr(), T, HV,
+                                              cu.data_ptr(), I32, self.NSEQ, 64, st), lib)
+                _ok(lib.xk_chunk_scaled_dot_kkt(k.data_ptr(), BF, beta.data_ptr(), BF,
+                                                b["gc"].data_ptr(), b["A"].data_ptr(), T, H, HV,
+                                                K, cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                _ok(lib.xk_solve_tril(b["A"].data_ptr(), b["Ai"].data_ptr(), BF, T, HV,
+                                      cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                _ok(lib.xk_recompute_w_u(k.data_ptr(), v.data_ptr(), BF, beta.data_ptr(), BF,
+                                         b["gc"].data_ptr(), b["Ai"].data_ptr(), BF,
+                                         b["w"].data_ptr(), b["u"].data_ptr(), T, H, HV, K, V,
+                                         cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                _ok(lib.xk_chunk_fwd_h(k.data_ptr(), b["w"].data_ptr(), b["u"].data_ptr(), BF,
+                                       b["gc"].data_ptr(), h0.data_ptr(), b["h"].data_ptr(), nt,
+                                       b["vn"].data_ptr(), b["ht"].data_ptr(), T, H, HV, K, V,
+                                       cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                _ok(lib.xk_chunk_fwd_o(q.data_ptr(), k.data_ptr(), b["vn"].data_ptr(),
+                                       b["h"].data_ptr(), nt, BF, b["gc"].data_ptr(),
+                                       b["o"].data_ptr(), self.K ** -0.5, T, H, HV, K, V,
+                                       cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+            out.append(run)
+        return out
+
+
+class L2NormCase(Case):
+    name = "l2norm_last_dim"
+    config = ("a6a (npu_l2norm_last_dim) on the prefill shape: q or k of config 4 as "
+              "rows, bf16 [262144, 128] (16384 tokens x 16 heads), eps 1e-6, bf16 out")
+    kernel = "l2norm_kernel"
+    timing = "graph"
+    R, C = 16384 * 16, 128
+    algo_bytes = R * C * 2 * 2
+
+    def __init__(self):
+        g = torch.Generator().manual_seed(0)
+        self.x = _randn((self.R, self.C), g, torch.bfloat16)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        out = []
+        for _ in range(n):
+            x = self.x.to(dev)
+            y = torch.empty_like(x)
+
+            def run(x=x, y=y):
+                _ok(lib.xk_l2norm_last_dim(x.data_ptr(), y.data_ptr(), self.R, self.C, 1e-6,
+                                           _lib.XK_BF16, _lib.XK_BF16, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import norm as on
+        x = self.x
+        return (lambda: on.l2norm_last_dim(x, 1e-6), "full shape, fp32 math on bf16 input", 1.0)
+
+
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
                              ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase,
-                             GdnChunkCase, GdnGatingCase, GdnSigmoidGatingCase,
-                             GatedRmsNormCase, QkvzbaSplitCase, RopeInplaceCase)}
+                             GdnChunkCase, GdnChunkStagedCase, GdnGatingCase,
+                             GdnSigmoidGatingCase, GatedRmsNormCase, QkvzbaSplitCase,
+                             RopeInplaceCase, L2NormCase)}
 HEADLINE = "layer_norm_fwd"
 
 

@@ -182,3 +182,24 @@ def test_l2norm_reference_shapes(dev, shape):
     torch.testing.assert_close(y.float().cpu(), ref, **BF16_TOL)
     y32 = ops.npu_l2norm_last_dim(x.to(dev), output_dtype=torch.float32)
     torch.testing.assert_close(y32.cpu(), ref, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("cols,dtype", [(8, torch.bfloat16), (128, torch.bfloat16),
+                                        (136, torch.bfloat16), (2048, torch.bfloat16),
+                                        (4096, torch.bfloat16), (100, torch.bfloat16),
+                                        (128, torch.float32), (1000, torch.float32),
+                                        (64, torch.float16)])
+def test_l2norm_row_widths(dev, cols, dtype):
+    # Every team width of the vector path (8 .. 2048 elements per 16-bit row,
+    # 128 and 1000 per fp32 row; 136 and 1000 leave lanes masked), and the
+    # per-row fallback for rows wider than 256 vectors (4096) or not a whole
+    # number of 16-byte vectors (100).
+    from torch_npu_ops_amd import ops
+    gen = torch.Generator().manual_seed(3)
+    x = _rand((301, cols), gen, dtype)
+    ref = on.l2norm_last_dim(x)
+    y = ops.npu_l2norm_last_dim(x.to(dev), output_dtype=torch.float32)
+    torch.testing.assert_close(y.cpu(), ref, rtol=1e-5, atol=1e-6)
+    yb = ops.npu_l2norm_last_dim(x.to(dev))
+    assert yb.dtype == dtype
+    torch.testing.assert_close(yb.float().cpu(), ref, **BF16_TOL)

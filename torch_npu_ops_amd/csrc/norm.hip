@@ -418,7 +418,8 @@ int run_norm_dtype(const NormParams& p, xk_dtype dt, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
-// L2 norm over the last dim: one wave per row, rows of any length.
+// L2 norm over the last dim.  Rows of aligned 16-byte vectors use the team
+// kernel below; other rows use one wave per row, of any length.
 // ---------------------------------------------------------------------------
 template <typename T, typename TO, int VEC>
 __global__ void __launch_bounds__(256)
@@ -446,9 +447,74 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Rows of up to 256 16-byte vectors: a team of TPG lanes per row holds the
+// row in registers (NV vectors per lane, one non-temporal read), reduces the
+// sum of squares with shuffles inside the team and writes once.  Teams are
+// at most a wave wide, so there is no LDS and no barrier; rows are
+// team-uniform, so a team that exits never leaves a partner lane behind.
+template <typename T, typename TO, int VEC, int TPG, int NV>
+__global__ void __launch_bounds__(256)
+    l2norm_team_kernel(const T* __restrict__ x, TO* __restrict__ y, int64_t rows,
+                       int cols, float eps) {
+  constexpr int kTeams = 256 / TPG;
+  const int team = threadIdx.x / TPG;
+  const int lane = threadIdx.x % TPG;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kTeams + team;
+  if (row >= rows) return;
+  using VT = Vec<T, VEC>;
+  using VO = Vec<TO, VEC>;
+  const T* xr = x + row * cols;
+  TO* yr = y + row * cols;
+  VT v[NV];
+  float s1 = 0.f, ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * TPG + lane) * VEC;
+    if (c < cols) {
+      v[j] = ld_stream(reinterpret_cast<const VT*>(xr + c));
+    } else {
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) v[j].v[u] = from_f32<T>(0.f);
+    }
+    vec_sums<T, VEC>(v[j], s1, ss);
+  }
+  const float r = 1.0f / sqrtf(group_sum<TPG>(ss) + eps);
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int c = (j * TPG + lane) * VEC;
+    if (c < cols) {
+      VO o;
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) o.v[u] = from_f32<TO>(to_f32(v[j].v[u]) * r);
+      st_stream(reinterpret_cast<VO*>(yr + c), o);
+    }
+  }
+}
+
+template <typename T, typename TO, int TPG, int NV>
+int launch_l2norm_team(const void* x, void* y, int64_t rows, int64_t cols, float eps,
+                       hipStream_t s) {
+  constexpr int kV = 16 / sizeof(T);
+  hipLaunchKernelGGL((l2norm_team_kernel<T, TO, kV, TPG, NV>), dim3(cdiv(rows, 256 / TPG)),
+                     dim3(256), 0, s, static_cast<const T*>(x), static_cast<TO*>(y), rows,
+                     static_cast<int>(cols), eps);
+  return launch_status();
+}
+
 template <typename T, typename TO>
 int run_l2norm(const void* x, void* y, int64_t rows, int64_t cols, float eps,
                hipStream_t s) {
+  constexpr int kV = 16 / sizeof(T);
+  if (cols % kV == 0 && aligned(x, 16) && aligned(y, kV * sizeof(TO)) &&
+      rows <= (int64_t{1} << 40)) {
+    const int64_t nvec = cols / kV;
+    if (nvec <= 8) return launch_l2norm_team<T, TO, 4, 2>(x, y, rows, cols, eps, s);
+    if (nvec <= 16) return launch_l2norm_team<T, TO, 8, 2>(x, y, rows, cols, eps, s);
+    if (nvec <= 32) return launch_l2norm_team<T, TO, 16, 2>(x, y, rows, cols, eps, s);
+    if (nvec <= 64) return launch_l2norm_team<T, TO, 32, 2>(x, y, rows, cols, eps, s);
+    if (nvec <= 128) return launch_l2norm_team<T, TO, 64, 2>(x, y, rows, cols, eps, s);
+    if (nvec <= 256) return launch_l2norm_team<T, TO, 64, 4>(x, y, rows, cols, eps, s);
+  }
   const dim3 grid(cdiv(rows, 4));
   const bool v4 = cols % 4 == 0 && aligned(x, 4 * sizeof(T)) &&
                   aligned(y, 4 * sizeof(TO));
