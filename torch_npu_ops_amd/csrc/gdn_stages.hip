@@ -40,7 +40,8 @@ struct Seq {
 };
 
 // ---------------------------------------------------------------------------
-// Per-chunk cumsum.  One thread per (token, head).
+// Per-chunk cumsum.  Chunks longer than 64: one thread per (token, head)
+// summing its chunk prefix.
 // ---------------------------------------------------------------------------
 struct CumsumParams : Seq {
   const void* g;
@@ -67,6 +68,62 @@ __global__ void __launch_bounds__(kTh) chunk_cumsum_kernel(CumsumParams p) {
     for (int64_t j = cs; j <= t; ++j) acc += ldf<GT>(p.g, j * p.H + h);
   }
   p.out[idx] = acc;
+}
+
+// Chunk sizes up to 64: one wave per (64-token block, head).  Each lane
+// loads one g, a segmented wave scan (segments = chunks) sums within the
+// block, and the tokens of lane 0's chunk that precede the block (at most
+// 63) are summed once and added to that chunk's lanes.  Every g is read
+// about twice instead of up to 64 times, and cu_seqlens is searched in LDS
+// (up to kScanLdsSeqs sequences) so no lane waits on a chain of global
+// reads.
+constexpr int64_t kScanLdsSeqs = 1023;
+
+// Start of the sequence holding token t, or -1; cu(i) reads cu_seqlens.
+template <class CU>
+__device__ __forceinline__ int64_t seq_start_of(const Seq& p, int64_t t, CU cu) {
+  if (t >= p.T || t < cu(0) || t >= cu(p.N)) return -1;
+  int64_t lo = 0, hi = p.N;  // cu[lo] <= t < cu[hi]
+  while (hi - lo > 1) {
+    const int64_t mid = (lo + hi) >> 1;
+    if (cu(mid) <= t) lo = mid; else hi = mid;
+  }
+  return cu(lo);
+}
+
+template <typename GT>
+__global__ void __launch_bounds__(kTh) chunk_cumsum_scan_kernel(CumsumParams p) {
+  __shared__ int64_t scu[kScanLdsSeqs + 1];
+  const bool small = p.N <= kScanLdsSeqs;
+  if (small)
+    for (int64_t i = threadIdx.x; i <= p.N; i += kTh) scu[i] = cu_at(p, i);
+  __syncthreads();
+  auto cu = [&](int64_t i) { return small ? scu[i] : cu_at(p, i); };
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t wv = static_cast<int64_t>(blockIdx.x) * (kTh / kWave) + (threadIdx.x >> 6);
+  const int64_t tb = wv / p.H;
+  const int h = static_cast<int>(wv - tb * p.H);
+  const int64_t t0 = tb * kWave;
+  if (t0 >= p.T) return;  // wave-uniform, after the block's only barrier
+  const int64_t t = t0 + lane;
+  const int64_t bos = seq_start_of(p, t, cu);
+  const int64_t cs = bos >= 0 ? bos + ((t - bos) / p.chunk) * p.chunk : t;
+  float x = bos >= 0 ? ldf<GT>(p.g, t * p.H + h) : 0.f;
+  // Lane l's segment starts at lane max(cs - t0, 0); tokens outside every
+  // sequence are segments of their own (and stay 0).
+  const int seg0 = static_cast<int>(max<int64_t>(cs - t0, 0));
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const float y = __shfl_up(x, o, kWave);
+    if (lane - o >= seg0) x += y;
+  }
+  const int64_t bos0 = seq_start_of(p, t0, cu);
+  const int64_t cs0 = bos0 >= 0 ? bos0 + ((t0 - bos0) / p.chunk) * p.chunk : t0;
+  float c = 0.f;
+  if (cs0 + lane < t0) c = ldf<GT>(p.g, (cs0 + lane) * p.H + h);
+  c = group_sum<kWave>(c);
+  if (bos >= 0 && cs == cs0) x += c;
+  if (t < p.T) p.out[t * p.H + h] = x;
 }
 
 // ---------------------------------------------------------------------------
@@ -599,8 +656,18 @@ extern "C" int xk_chunk_local_cumsum(const void* g, xk_dtype g_dtype, float* out
   p.out = out;
   p.H = static_cast<int>(H);
   p.chunk = static_cast<int>(chunk_size);
-  const int64_t blocks = cdiv(total_tokens * H, kTh);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (chunk_size <= kC) {
+    const int64_t blocks = cdiv(cdiv(total_tokens, kWave) * H, kTh / kWave);
+    switch (g_dtype) {
+      case XK_F32: hipLaunchKernelGGL(chunk_cumsum_scan_kernel<float>, dim3(blocks), dim3(kTh), 0, s, p); break;
+      case XK_BF16: hipLaunchKernelGGL(chunk_cumsum_scan_kernel<bf16>, dim3(blocks), dim3(kTh), 0, s, p); break;
+      case XK_F16: hipLaunchKernelGGL(chunk_cumsum_scan_kernel<f16>, dim3(blocks), dim3(kTh), 0, s, p); break;
+      default: return XK_ERR_UNSUPPORTED;
+    }
+    return launch_status();
+  }
+  const int64_t blocks = cdiv(total_tokens * H, kTh);
   switch (g_dtype) {
     case XK_F32: hipLaunchKernelGGL(chunk_cumsum_kernel<float>, dim3(blocks), dim3(kTh), 0, s, p); break;
     case XK_BF16: hipLaunchKernelGGL(chunk_cumsum_kernel<bf16>, dim3(blocks), dim3(kTh), 0, s, p); break;
