@@ -519,13 +519,24 @@ struct FwdOParams : Seq {
 template <int K, int V>
 struct __align__(16) FwdOSmem {
   __bf16 ht[V][K + 8];   // h_c transposed: ht[v][k]
-  __bf16 vt[V][kLt];     // v_new transposed: vt[v][token]
-  __bf16 aq[kC][kLt];    // masked q k^T, row-major
+  __bf16 vt[V][kLt];     // v_new transposed: vt[v][token]; rows >= L zero
   float gc[kC];
 };
 
+// One block per (chunk, head); wave w produces the outputs of tokens
+// 16w .. 16w + 15.  Everything is computed transposed, o^T = h^T q^T +
+// v^T Aq^T, so that a lane owns one token and 4 consecutive columns of it
+// (one 8-byte store per 16 columns):
+//  * h and v_new reach LDS transposed through select_op MFMAs (exact), as
+//    8-byte vectors;
+//  * Aq^T = (k q^T masked and decayed, rounded to bf16 as the reference's
+//    A.to(v), chunk_o.py:113) stays in registers: its MFMA C layout holds 4
+//    consecutive key tokens per lane, and two such tiles form the B operand
+//    with the key tokens in the order {4g .. 4g+3, 16+4g .. 16+4g+3}; the
+//    matching A operand reads the same tokens of vt as two 8-byte halves.
 template <int K, int V>
 __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
+  static_assert(K == 128 && V == 128, "head dims of 128");
   __shared__ FwdOSmem<K, V> sm;
   constexpr int KK = K / 32, NJ = V / 16;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
@@ -536,69 +547,119 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
   int L;
   if (!locate_chunk(p, c, n, s, L) || c >= p.hcap) return;  // block-uniform
   const int hq = h / (p.H / p.Hg);
+  const bf8_t sel[2] = {select_op(0), select_op(1)};
+  const f4_t zero = {0.f, 0.f, 0.f, 0.f};
+
+  // h_c rows 32w .. 32w + 31 -> ht (transposed).
   const bf16* hsrc = reinterpret_cast<const bf16*>(p.h) + (c * p.H + h) * static_cast<int64_t>(K) * V;
-  for (int i = tid; i < K * (V / 8); i += kTh) {
-    const int kr = i / (V / 8), c0 = (i % (V / 8)) * 8;
-    const Vec<bf16, 8> x = *reinterpret_cast<const Vec<bf16, 8>*>(hsrc + kr * V + c0);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sm.ht[c0 + e][kr] = x.v[e];
+  for (int mt = 0; mt < 2; ++mt) {
+    const int k0 = wid * 32 + mt * 16;
+    bf8_t a[V / 32];
+#pragma unroll
+    for (int kk = 0; kk < V / 32; ++kk)
+      a[kk] = *reinterpret_cast<const bf8_t*>(hsrc + (k0 + l15) * V + kk * 32 + 8 * lg);
+#pragma unroll
+    for (int kk = 0; kk < V / 32; ++kk)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const f4_t t = mfma16(a[kk], sel[hh], zero);
+        Vec<__bf16, 4> b;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(t[i]);
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.ht[kk * 32 + hh * 16 + l15][k0 + 4 * lg]) = b;
+      }
   }
-  const bf16* vsrc = reinterpret_cast<const bf16*>(p.v) + (s * p.H + h) * static_cast<int64_t>(V);
-  for (int i = tid; i < kC * (V / 8); i += kTh) {
-    const int t = i / (V / 8), c0 = (i % (V / 8)) * 8;
-    Vec<bf16, 8> x = *reinterpret_cast<const Vec<bf16, 8>*>(
-        vsrc + static_cast<int64_t>(min(t, L - 1)) * p.H * V + c0);
+  // v_new rows (tokens) 16w .. 16w + 15 -> vt (transposed), rows >= L zero.
+  {
+    const int t = wid * 16 + l15;
+    const bf16* vsrc = reinterpret_cast<const bf16*>(p.v) +
+                       ((s + min(t, L - 1)) * p.H + h) * static_cast<int64_t>(V);
+    bf8_t a[V / 32];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) sm.vt[c0 + e][t] = t < L ? x.v[e] : static_cast<bf16>(0.f);
+    for (int kk = 0; kk < V / 32; ++kk) {
+      a[kk] = *reinterpret_cast<const bf8_t*>(vsrc + kk * 32 + 8 * lg);
+      if (t >= L) a[kk] = bf8_t{};
+    }
+#pragma unroll
+    for (int kk = 0; kk < V / 32; ++kk)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const f4_t r = mfma16(a[kk], sel[hh], zero);
+        Vec<__bf16, 4> b;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(r[i]);
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.vt[kk * 32 + hh * 16 + l15][wid * 16 + 4 * lg]) = b;
+      }
   }
   if (tid < kC) sm.gc[tid] = p.gcum ? p.gcum[(s + min(tid, L - 1)) * p.H + h] : 0.f;
   __syncthreads();
 
   const int64_t qrow = static_cast<int64_t>(p.Hg) * K;
+  const int tq = wid * 16 + l15;  // this lane's output token
   bf8_t qa[KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
     qa[kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, qrow, wid * 16, kk);
-  // Masked q k^T rows of this wave -> aq (bf16, as the reference's A.to(v)).
+  const float gq = sm.gc[tq];
+
+  // Aq^T tiles (key tokens 16j + 4lg + i, query token tq), j <= w.
+  f4_t at[4];
 #pragma unroll
-  for (int nj = 0; nj < 4; ++nj) {
-    f4_t a = {0.f, 0.f, 0.f, 0.f};
-    if (nj <= wid) {
+  for (int j = 0; j < 4; ++j) {
+    at[j] = zero;
+    if (j <= wid) {
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk)
-        a = mfma16(qa[kk], load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, qrow, nj * 16, kk), a);
-    }
+        at[j] = mfma16(load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, qrow, j * 16, kk),
+                       qa[kk], at[j]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wid * 16 + 4 * lg + i, col = nj * 16 + l15;
-      float val = 0.f;
-      if (nj <= wid && row >= col && col < L)
-        val = a[i] * (p.gcum ? safe_exp(sm.gc[row] - sm.gc[col]) : 1.f);
-      sm.aq[row][col] = static_cast<__bf16>(val);
+      for (int i = 0; i < 4; ++i) {
+        const int tk = j * 16 + 4 * lg + i;
+        const bool keep = tk <= tq && tq < L;
+        at[j][i] = keep ? at[j][i] * (p.gcum ? safe_exp(gq - sm.gc[tk]) : 1.f) : 0.f;
+      }
     }
   }
-  __builtin_amdgcn_wave_barrier();  // this wave's aq rows are its own
-  bf16* o = reinterpret_cast<bf16*>(p.o);
+  // B operands: key tokens {32m + 4lg .. +3, 32m + 16 + 4lg .. +3}, bf16.
+  bf8_t aqb[2];
 #pragma unroll
-  for (int nj = 0; nj < NJ; ++nj) {
-    f4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      acc = mfma16(qa[kk], *reinterpret_cast<const bf8_t*>(&sm.ht[nj * 16 + l15][kk * 32 + 8 * lg]), acc);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] *= p.gcum ? __expf(sm.gc[wid * 16 + 4 * lg + i]) : 1.f;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      if (kk * 32 > wid * 16 + 15) continue;  // beyond the diagonal
-      acc = mfma16(*reinterpret_cast<const bf8_t*>(&sm.aq[wid * 16 + l15][kk * 32 + 8 * lg]),
-                   *reinterpret_cast<const bf8_t*>(&sm.vt[nj * 16 + l15][kk * 32 + 8 * lg]), acc);
-    }
+  for (int m = 0; m < 2; ++m)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = wid * 16 + 4 * lg + i;
-      if (row < L)
-        o[((s + row) * p.H + h) * static_cast<int64_t>(V) + nj * 16 + l15] =
-            from_f32<bf16>(p.scale * acc[i]);
+      aqb[m][i] = static_cast<__bf16>(at[2 * m][i]);
+      aqb[m][4 + i] = static_cast<__bf16>(at[2 * m + 1][i]);
+    }
+
+  const float eg = p.gcum ? __expf(gq) : 1.f;
+  bf16* orow = reinterpret_cast<bf16*>(p.o) + ((s + min(tq, L - 1)) * p.H + h) * static_cast<int64_t>(V);
+#pragma unroll
+  for (int nj = 0; nj < NJ; ++nj) {
+    f4_t acc = zero;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      acc = mfma16(*reinterpret_cast<const bf8_t*>(&sm.ht[nj * 16 + l15][kk * 32 + 8 * lg]),
+                   qa[kk], acc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] *= eg;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      if (m * 32 > wid * 16 + 15) continue;  // key tokens beyond the diagonal
+      const Vec<__bf16, 4> lo = *reinterpret_cast<const Vec<__bf16, 4>*>(&sm.vt[nj * 16 + l15][m * 32 + 4 * lg]);
+      const Vec<__bf16, 4> hi = *reinterpret_cast<const Vec<__bf16, 4>*>(&sm.vt[nj * 16 + l15][m * 32 + 16 + 4 * lg]);
+      bf8_t va;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        va[i] = lo.v[i];
+        va[4 + i] = hi.v[i];
+      }
+      acc = mfma16(va, aqb[m], acc);
+    }
+    if (tq < L) {
+      Vec<bf16, 4> ov;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ov.v[i] = from_f32<bf16>(p.scale * acc[i]);
+      *reinterpret_cast<Vec<bf16, 4>*>(orow + nj * 16 + 4 * lg) = ov;
     }
   }
 }
@@ -814,7 +875,8 @@ extern "C" int xk_chunk_fwd_o(const void* q, const void* k, const void* v, const
   if (dtype != XK_BF16 || K != 128 || V != 128) return XK_ERR_UNSUPPORTED;
   if (N == 0 || total_tokens == 0) return XK_OK;
   if (!q || !k || !v || !h || !o || !cu_seqlens) return XK_ERR_INVALID;
-  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(h, 16))
+  if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(h, 16) ||
+      !aligned(o, 8))
     return XK_ERR_INVALID;
   p.q = q;
   p.k = k;
