@@ -239,102 +239,108 @@ struct WuParams : Seq {
 
 constexpr int kLt = kC + 8;  // bf16 LDS row stride (144 B: 16-byte aligned)
 
-template <int D, typename AT>
-__device__ __forceinline__ void wu_product(const WuParams& p, __bf16 (*bt)[D][kLt], int64_t s,
-                                           int L, int h, void* out) {
-  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int l15 = lane & 15, lg = lane >> 4;
-  constexpr int NJ = D / 64;  // 16-column tiles per wave
-  f4_t acc[4][NJ];
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int nj = 0; nj < NJ; ++nj) acc[mi][nj] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) {
-    const AT* arow = reinterpret_cast<const AT*>(p.Ai) +
-                     ((s + min(mi * 16 + l15, L - 1)) * p.H + h) * kC + 8 * lg;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      bf8_t ah, al;
-      if constexpr (std::is_same<AT, float>::value) {
-        split8(arow + kk * 32, ah, al);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          ah[e] = static_cast<__bf16>(to_f32(arow[kk * 32 + e]));
-          al[e] = static_cast<__bf16>(0.f);
-        }
-      }
-#pragma unroll
-      for (int nj = 0; nj < NJ; ++nj) {
-        const int col = wid * (D / 4) + nj * 16 + l15;
-        const bf8_t bh = *reinterpret_cast<const bf8_t*>(&bt[0][col][kk * 32 + 8 * lg]);
-        const bf8_t bl = *reinterpret_cast<const bf8_t*>(&bt[1][col][kk * 32 + 8 * lg]);
-        acc[mi][nj] = mfma16(ah, bh, acc[mi][nj]);
-        acc[mi][nj] = mfma16(ah, bl, acc[mi][nj]);
-        if constexpr (std::is_same<AT, float>::value) acc[mi][nj] = mfma16(al, bh, acc[mi][nj]);
-      }
-    }
-  }
-  bf16* o = reinterpret_cast<bf16*>(out);
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int nj = 0; nj < NJ; ++nj)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = mi * 16 + 4 * lg + i;
-        if (row < L)
-          o[((s + row) * p.H + h) * D + wid * (D / 4) + nj * 16 + l15] = from_f32<bf16>(acc[mi][nj][i]);
-      }
-}
-
-// Rows t < L of src (row stride `rs`, bf16) times f[t] into bt (transposed,
-// hi / lo); rows >= L are zero.
-template <int D>
-__device__ __forceinline__ void stage_scaled_t(__bf16 (*bt)[D][kLt], const bf16* src, int64_t rs,
-                                               const float* f, int L) {
-  for (int i = threadIdx.x; i < kC * (D / 8); i += kTh) {
-    const int t = i / (D / 8), c0 = (i % (D / 8)) * 8;
-    const Vec<bf16, 8> x = *reinterpret_cast<const Vec<bf16, 8>*>(src + min(t, L - 1) * rs + c0);
-    const float sc = t < L ? f[t] : 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      __bf16 hi, lo;
-      split(sc * to_f32(x.v[e]), hi, lo);
-      bt[0][c0 + e][t] = hi;
-      bt[1][c0 + e][t] = lo;
-    }
-  }
-}
+// One block per (chunk, head); wave w owns tokens 16w .. 16w + 15 of both
+// products.  Each product is formed transposed, out^T = rhs^T Ai^T, so a
+// lane owns one token and 4 consecutive columns of it (8-byte stores), and
+// the wave's Ai rows are the B operands of both products (loaded once).
+// The right-hand sides (v beta and k beta exp(gc), fp32) reach LDS
+// transposed as hi / lo bf16: the wave's 16 token rows go through
+// select_op MFMAs (exact), are scaled per token in the MFMA C layout and
+// split there, and leave as 8-byte vectors.  Ai is lower triangular, so
+// waves 0 and 1 skip the key tokens 32 .. 63.
 
 template <typename BT, typename AT>
 __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
   constexpr int D = 128;  // K = V = 128
-  __shared__ __align__(16) __bf16 bt[2][D][kLt];
+  __shared__ __align__(16) __bf16 bt[2][D][kLt];  // rhs^T hi / lo: bt[.][d][token]
   __shared__ float fb[kC], fk[kC];
   const int h = blockIdx.y;
   int64_t n, s;
   int L;
   if (!locate_chunk(p, blockIdx.x, n, s, L)) return;  // block-uniform
   const int hq = h / (p.H / p.Hg);
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
   if (threadIdx.x < kC) {
     const int t = min(static_cast<int>(threadIdx.x), L - 1);
     const float b = ldf<BT>(p.beta, (s + t) * p.H + h);
     fb[threadIdx.x] = b;
     fk[threadIdx.x] = b * __expf(p.gcum ? p.gcum[(s + t) * p.H + h] : 0.f);
   }
-  __syncthreads();
-  stage_scaled_t<D>(bt, reinterpret_cast<const bf16*>(p.v) + (s * p.H + h) * D,
-                    static_cast<int64_t>(p.H) * D, fb, L);
-  __syncthreads();
-  wu_product<D, AT>(p, bt, s, L, h, p.u);
-  __syncthreads();
-  stage_scaled_t<D>(bt, reinterpret_cast<const bf16*>(p.k) + (s * p.Hg + hq) * D,
-                    static_cast<int64_t>(p.Hg) * D, fk, L);
-  __syncthreads();
-  wu_product<D, AT>(p, bt, s, L, h, p.w);
+  const int tq = wid * 16 + l15;  // this lane's token
+  // Ai row tq (B operands), hi / lo for fp32 Ai.
+  const AT* arow = reinterpret_cast<const AT*>(p.Ai) + ((s + min(tq, L - 1)) * p.H + h) * kC + 8 * lg;
+  bf8_t aih[2], ail[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    if constexpr (std::is_same<AT, float>::value) {
+      split8(arow + kk * 32, aih[kk], ail[kk]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        aih[kk][e] = static_cast<__bf16>(to_f32(arow[kk * 32 + e]));
+        ail[kk][e] = static_cast<__bf16>(0.f);
+      }
+    }
+  }
+  const bf8_t sel[2] = {select_op(0), select_op(1)};
+  const f4_t zero = {0.f, 0.f, 0.f, 0.f};
+  __syncthreads();  // fb / fk
+
+#pragma unroll 1
+  for (int prod = 0; prod < 2; ++prod) {
+    // prod 0: u = Ai (v beta); prod 1: w = Ai (k beta exp(gc)).
+    const bf16* src = prod == 0
+        ? reinterpret_cast<const bf16*>(p.v) + ((s + min(tq, L - 1)) * p.H + h) * D
+        : reinterpret_cast<const bf16*>(p.k) + ((s + min(tq, L - 1)) * p.Hg + hq) * D;
+    const float* f = prod == 0 ? fb : fk;
+    bf8_t a[D / 32];
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk) {
+      a[kk] = *reinterpret_cast<const bf8_t*>(src + kk * 32 + 8 * lg);
+      if (tq >= L) a[kk] = bf8_t{};
+    }
+    f4_t fr;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) fr[i] = f[wid * 16 + 4 * lg + i];
+#pragma unroll
+    for (int kk = 0; kk < D / 32; ++kk)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        f4_t x = mfma16(a[kk], sel[hh], zero);  // tokens 16w + 4lg + i, column 32kk + 16hh + l15
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] *= fr[i];
+        Vec<__bf16, 4> xh, xl;
+        split4(x, xh, xl);
+        const int d = kk * 32 + hh * 16 + l15;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&bt[0][d][wid * 16 + 4 * lg]) = xh;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&bt[1][d][wid * 16 + 4 * lg]) = xl;
+      }
+    __syncthreads();  // bt complete
+
+    bf16* orow = reinterpret_cast<bf16*>(prod == 0 ? p.u : p.w) +
+                 ((s + min(tq, L - 1)) * p.H + h) * D;
+#pragma unroll
+    for (int nj = 0; nj < D / 16; ++nj) {
+      f4_t acc = zero;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        if (kk * 32 > wid * 16 + 15) continue;  // key tokens beyond the diagonal
+        const bf8_t bh = *reinterpret_cast<const bf8_t*>(&bt[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t bl = *reinterpret_cast<const bf8_t*>(&bt[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+        acc = mfma16(bh, aih[kk], acc);
+        acc = mfma16(bl, aih[kk], acc);
+        if constexpr (std::is_same<AT, float>::value) acc = mfma16(bh, ail[kk], acc);
+      }
+      if (tq < L) {
+        Vec<bf16, 4> ov;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov.v[i] = from_f32<bf16>(acc[i]);
+        *reinterpret_cast<Vec<bf16, 4>*>(orow + nj * 16 + 4 * lg) = ov;
+      }
+    }
+    __syncthreads();  // bt reads done before the next product overwrites it
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -806,7 +812,9 @@ extern "C" int xk_recompute_w_u(const void* k, const void* v, xk_dtype dtype, co
   if (ai_dtype != XK_BF16 && ai_dtype != XK_F32) return XK_ERR_UNSUPPORTED;
   if (N == 0 || total_tokens == 0) return XK_OK;
   if (!k || !v || !beta || !Ai || !w || !u || !cu_seqlens) return XK_ERR_INVALID;
-  if (!aligned(k, 16) || !aligned(v, 16) || !aligned(Ai, 16)) return XK_ERR_INVALID;
+  if (!aligned(k, 16) || !aligned(v, 16) || !aligned(Ai, 16) || !aligned(w, 8) ||
+      !aligned(u, 8))
+    return XK_ERR_INVALID;
   p.k = k;
   p.v = v;
   p.beta = beta;
