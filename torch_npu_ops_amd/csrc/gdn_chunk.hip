@@ -365,29 +365,6 @@ __device__ __forceinline__ void load_out(const ChunkParams& p, OutOps<K / 32>& o
   ops.cq = sc[0 * kC + wid * 16 + l15];
 }
 
-// K rows of the lane's A operands written transposed, kt[k][token]: the
-// select_op MFMAs hand each lane 4 consecutive tokens of one key column,
-// stored as one 8-byte vector (bank-conflict-free at the kLt row stride).
-template <int K>
-__device__ __forceinline__ void store_kt(__bf16 (*kt)[kLt], const bf8_t (&kA)[K / 32],
-                                         const bf8_t (&sel)[2]) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int l15 = lane & 15, lg = lane >> 4;
-#pragma unroll
-  for (int kk = 0; kk < K / 32; ++kk)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const f4_t c = mfma16(kA[kk], sel[h], f4_t{0.f, 0.f, 0.f, 0.f});
-      Vec<__bf16, 4> b;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(c[i]);
-      *reinterpret_cast<Vec<__bf16, 4>*>(&kt[kk * 32 + 16 * h + l15][wid * 16 + 4 * lg]) = b;
-    }
-}
-
-// BV = 32: two waves per SIMD (<= 256 registers per lane), two blocks share
-// a CU.  BV = 64: one wave per SIMD with up to 512 registers; every loaded
-// K / Q / Ai / Aq operand serves twice the columns.
 template <int K, typename T, int BV>
 __global__ void __launch_bounds__(kTh) __attribute__((amdgpu_waves_per_eu(BV == 32 ? 2 : 1)))
 gdn_chunk_state_kernel(ChunkParams p, int nvt) {
@@ -463,7 +440,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     load_inv(p, inv, cidx0, hv);
     __builtin_amdgcn_sched_barrier(0);
     load_out<K>(p, outo, bos, L0, cidx0, hv, hq);
-    store_kt<K>(sm.kt[0], opsA.kA, sel);
+    store_kt<K, kLt>(sm.kt[0], opsA.kA, sel);
   }
   __syncthreads();
 
@@ -604,7 +581,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       }
     }
     publish_state();
-    store_kt<K>(sm.kt[(ci + 1) & 1], nxt.kA, sel);
+    store_kt<K, kLt>(sm.kt[(ci + 1) & 1], nxt.kA, sel);
     __syncthreads();  // (3) state copy, next keys complete; vt / dt / kt reads done
   };
   // Unrolled by two so the operand buffers swap roles without copies.

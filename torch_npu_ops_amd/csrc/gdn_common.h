@@ -95,6 +95,26 @@ __device__ __forceinline__ bf8_t select_op(int h) {
   return b;
 }
 
+// Keys of the lane's A operands (rows wave*16 + lane%16, 32 columns per
+// operand) written transposed, kt[k][token], as 8-byte vectors: select_op
+// MFMAs hand each lane 4 consecutive tokens of one key column.
+template <int K, int LD>
+__device__ __forceinline__ void store_kt(__bf16 (*kt)[LD], const bf8_t (&kA)[K / 32],
+                                         const bf8_t (&sel)[2]) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int l15 = lane & 15, lg = lane >> 4;
+#pragma unroll
+  for (int kk = 0; kk < K / 32; ++kk)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f4_t c = mfma16(kA[kk], sel[h], f4_t{0.f, 0.f, 0.f, 0.f});
+      Vec<__bf16, 4> b;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(c[i]);
+      *reinterpret_cast<Vec<__bf16, 4>*>(&kt[kk * 32 + 16 * h + l15][wid * 16 + 4 * lg]) = b;
+    }
+}
+
 // (ah + al)(bh + bl) without the lo*lo term.
 __device__ __forceinline__ f4_t mfma_split3(const bf8_t& ah, const bf8_t& al, const bf8_t& bh,
                                             const bf8_t& bl, f4_t c) {

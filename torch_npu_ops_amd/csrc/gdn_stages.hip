@@ -372,6 +372,17 @@ struct __align__(16) FwdHSmem {
   float gc[kC];
 };
 
+// One chunk's global operands for this lane, loaded a chunk ahead: key rows
+// and w rows wave*16 + lane%16 (A layout), the lane's u row in A layout
+// (select_op turns it into C layout) and, for lanes < 64, one token's gc.
+template <int KK>
+struct FwdHOps {
+  bf8_t ka[KK];
+  bf8_t wa[KK];
+  bf8_t ua;
+  float gct;
+};
+
 template <int K>
 __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
   __shared__ FwdHSmem<K> sm;
@@ -403,10 +414,30 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
         sreg[m2][nj][i] = p.h0 ? p.h0[((n * p.H + h) * K + kr) * V + v0 + nj * 16 + l15] : 0.f;
       }
   const int64_t krow = static_cast<int64_t>(p.Hg) * K;
-  for (int64_t ci = 0; ci < nch; ++ci) {
+  const int64_t wrow = static_cast<int64_t>(p.H) * K;
+  const bf8_t sel[2] = {select_op(0), select_op(1)};
+  auto load_ops = [&](FwdHOps<KK>& o, int64_t ci) {
+    const int64_t s = bos + ci * kC;
+    const int L = static_cast<int>(min<int64_t>(kC, eos - s));
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      o.ka[kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, krow, wid * 16, kk);
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      o.wa[kk] = load_rows_op(p.w, static_cast<int64_t>(h) * K, s, L, wrow, wid * 16, kk);
+    o.ua = *reinterpret_cast<const bf8_t*>(
+        reinterpret_cast<const bf16*>(p.u) +
+        ((s + min(wid * 16 + l15, L - 1)) * p.H + h) * static_cast<int64_t>(V) + v0 + 8 * lg);
+    o.gct = p.gcum ? p.gcum[(s + min(tid & (kC - 1), L - 1)) * p.H + h] : 0.f;
+  };
+
+  // One chunk; `cur` holds its operands, `nxt` receives the next chunk's
+  // (the last chunk loads itself again, so every load is unconditional).
+  auto step = [&](const FwdHOps<KK>& cur, FwdHOps<KK>& nxt, int64_t ci) {
     const int64_t s = bos + ci * kC;
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
     const int64_t cidx = c0 + ci;
+    load_ops(nxt, min(ci + 1, nch - 1));
     // Snapshot of the state entering this chunk, and its bf16 hi / lo copy.
     bf16* hdst = reinterpret_cast<bf16*>(p.h) + (cidx * p.H + h) * static_cast<int64_t>(K) * V;
 #pragma unroll
@@ -418,50 +449,45 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
         for (int i = 0; i < 4; ++i) {
           const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
           hdst[static_cast<int64_t>(kr) * V + v0 + nj * 16 + l15] = from_f32<bf16>(sreg[m2][nj][i]);
-          split(sreg[m2][nj][i], hi.v[i], lo.v[i]);
         }
+        split4(sreg[m2][nj], hi, lo);
         const int k0 = wid * (K / 4) + m2 * 16 + 4 * lg;
         *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][nj * 16 + l15][k0]) = hi;
         *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[1][nj * 16 + l15][k0]) = lo;
       }
-    // Keys transposed; per-token gc.
-    bf8_t ka[KK];
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      ka[kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, krow, wid * 16, kk);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) sm.kt[kk * 32 + 8 * lg + e][wid * 16 + l15] = ka[kk][e];
-    }
-    if (tid < kC) sm.gc[tid] = p.gcum ? p.gcum[(s + min(tid, L - 1)) * p.H + h] : 0.f;
+    store_kt<K, kLt>(sm.kt, cur.ka, sel);
+    if (tid < kC) sm.gc[tid] = cur.gct;
     __syncthreads();
     // WS = w S (hi / lo S) for rows wid*16.., then v_new = u - WS.
     f4_t ws[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const bf8_t wa = load_rows_op(p.w, static_cast<int64_t>(h) * K, s, L,
-                                    static_cast<int64_t>(p.H) * K, wid * 16, kk);
+    for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
       for (int nj = 0; nj < 2; ++nj) {
         const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
         const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][kk * 32 + 8 * lg]);
-        ws[nj] = mfma16(wa, sh, ws[nj]);
-        ws[nj] = mfma16(wa, sl, ws[nj]);
+        ws[nj] = mfma16(cur.wa[kk], sh, ws[nj]);
+        ws[nj] = mfma16(cur.wa[kk], sl, ws[nj]);
       }
-    }
     const float gl = sm.gc[L - 1];
 #pragma unroll
     for (int nj = 0; nj < 2; ++nj) {
+      const f4_t uc = mfma16(cur.ua, sel[nj], f4_t{0.f, 0.f, 0.f, 0.f});
       Vec<__bf16, 4> dh, dl;
+      f4_t d;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = wid * 16 + 4 * lg + i;
-        const int rr = min(row, L - 1);
-        const int64_t off = ((s + rr) * p.H + h) * static_cast<int64_t>(V) + v0 + nj * 16 + l15;
-        const float vn = to_f32(reinterpret_cast<const bf16*>(p.u)[off]) - ws[nj][i];
-        if (p.vnew && row < L) reinterpret_cast<bf16*>(p.vnew)[off] = from_f32<bf16>(vn);
+        const float vn = uc[i] - ws[nj][i];
+        // Rows >= L repeat row L-1 (their operands are clamped to it), so
+        // storing them at row L-1 rewrites the same value.
+        if (p.vnew)
+          reinterpret_cast<bf16*>(p.vnew)[((s + min(row, L - 1)) * p.H + h) * static_cast<int64_t>(V) +
+                                          v0 + nj * 16 + l15] = from_f32<bf16>(vn);
         const float dec = row < L ? (p.gcum ? safe_exp(gl - sm.gc[row]) : 1.f) : 0.f;
-        split(vn * dec, dh.v[i], dl.v[i]);
+        d[i] = vn * dec;
       }
+      split4(d, dh, dl);
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = dh;
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[1][nj * 16 + l15][wid * 16 + 4 * lg]) = dl;
     }
@@ -491,6 +517,13 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
       }
     }
     __syncthreads();  // sb / kt / dt / gc are rewritten by the next chunk
+  };
+  FwdHOps<KK> opsA, opsB;
+  if (nch > 0) load_ops(opsA, 0);
+  // Unrolled by two so the operand buffers swap roles without copies.
+  for (int64_t ci = 0; ci < nch; ci += 2) {
+    step(opsA, opsB, ci);
+    if (ci + 1 < nch) step(opsB, opsA, ci + 1);
   }
   if (p.ht) {
 #pragma unroll
