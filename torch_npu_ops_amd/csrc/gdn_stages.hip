@@ -160,28 +160,35 @@ __global__ void __launch_bounds__(kTh) chunk_kkt_kernel(KktParams p) {
   vec[wid][0][lane] = p.gcum ? p.gcum[(s + lt) * p.H + h] : 0.f;
   vec[wid][1][lane] = ldf<BT>(p.beta, (s + lt) * p.H + h);
   __builtin_amdgcn_wave_barrier();
+  // K K^T is symmetric, so the MFMA of tile (nj, mi) holds tile (mi, nj)
+  // transposed: lane (l15, lg) gets row mi*16 + l15, columns nj*16 + 4lg ..
+  // + 3, stored as one 16-byte vector.
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < 4; ++mi) {
+    const int row = mi * 16 + l15;
+    const float brow = vec[wid][1][row], grow = vec[wid][0][row];
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       f4_t a = {0.f, 0.f, 0.f, 0.f};
       if (nj <= mi) {
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) a = mfma16(kop[mi][kk], kop[nj][kk], a);
+        for (int kk = 0; kk < KK; ++kk) a = mfma16(kop[nj][kk], kop[mi][kk], a);
       }
+      f4_t val;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = mi * 16 + 4 * lg + i, col = nj * 16 + l15;
-        if (row < L) {
-          float val = 0.f;
-          if (row > col) {
-            val = vec[wid][1][row] * a[i];
-            if (p.gcum) val *= safe_exp(vec[wid][0][row] - vec[wid][0][col]);
-          }
-          p.A[((s + row) * p.H + h) * kC + col] = val;
+        const int col = nj * 16 + 4 * lg + i;
+        float v = 0.f;
+        if (row > col) {
+          v = brow * a[i];
+          if (p.gcum) v *= safe_exp(grow - vec[wid][0][col]);
         }
+        val[i] = v;
       }
+      if (row < L)
+        *reinterpret_cast<f4_t*>(p.A + ((s + row) * p.H + h) * kC + nj * 16 + 4 * lg) = val;
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -202,22 +209,36 @@ __global__ void __launch_bounds__(kTh) solve_tril_kernel(TrilParams p) {
   int L;
   if (!(h < p.H && locate_chunk(p, blockIdx.x, n, s, L))) return;  // wave-uniform
   float (*X)[kLd] = lds[wid];
-  // Lane r loads row r (strictly lower part; rows >= L are zero).
-  const float* src = p.A + ((s + min(lane, L - 1)) * p.H + h) * kC;
+  // Access j covers rows 8j .. 8j + 7 (lane: row 8j + lane / 8, columns
+  // 8 (lane % 8) .. + 7), so every instruction moves whole rows.  Strictly
+  // lower part only; rows >= L are zero.
+  const int sr = lane >> 3, sc = (lane & 7) * 8;
 #pragma unroll
-  for (int j0 = 0; j0 < kC; j0 += 4) {
-    const f4_t a = *reinterpret_cast<const f4_t*>(src + j0);
-    f4_t m;
+  for (int j = 0; j < kC / 8; ++j) {
+    const int row = 8 * j + sr;
+    const float* src = p.A + ((s + min(row, L - 1)) * p.H + h) * kC + sc;
+    const f4_t a0 = *reinterpret_cast<const f4_t*>(src);
+    const f4_t a1 = *reinterpret_cast<const f4_t*>(src + 4);
+    f4_t m0, m1;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) m[e] = (lane < L && j0 + e < lane) ? a[e] : 0.f;
-    *reinterpret_cast<f4_t*>(&X[lane][j0]) = m;
+    for (int e = 0; e < 4; ++e) {
+      m0[e] = (row < L && sc + e < row) ? a0[e] : 0.f;
+      m1[e] = (row < L && sc + 4 + e < row) ? a1[e] : 0.f;
+    }
+    *reinterpret_cast<f4_t*>(&X[row][sc]) = m0;
+    *reinterpret_cast<f4_t*>(&X[row][sc + 4]) = m1;
   }
   __builtin_amdgcn_wave_barrier();
   invert_unit_lower(X);
-  if (lane < L) {
-    OT* dst = reinterpret_cast<OT*>(p.Ai) + ((s + lane) * p.H + h) * kC;
 #pragma unroll
-    for (int j = 0; j < kC; ++j) dst[j] = from_f32<OT>(X[lane][j]);
+  for (int j = 0; j < kC / 8; ++j) {
+    const int row = 8 * j + sr;
+    if (row < L) {
+      Vec<OT, 8> o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o.v[e] = from_f32<OT>(X[row][sc + e]);
+      *reinterpret_cast<Vec<OT, 8>*>(reinterpret_cast<OT*>(p.Ai) + ((s + row) * p.H + h) * kC + sc) = o;
+    }
   }
 }
 
@@ -789,7 +810,8 @@ extern "C" int xk_chunk_scaled_dot_kkt(const void* k, xk_dtype dtype, const void
   if (dtype != XK_BF16 || K != 128) return XK_ERR_UNSUPPORTED;
   if (beta_dtype != XK_BF16 && beta_dtype != XK_F32) return XK_ERR_UNSUPPORTED;
   if (N == 0 || total_tokens == 0) return XK_OK;
-  if (!k || !beta || !A || !cu_seqlens || !aligned(k, 16)) return XK_ERR_INVALID;
+  if (!k || !beta || !A || !cu_seqlens || !aligned(k, 16) || !aligned(A, 16))
+    return XK_ERR_INVALID;
   p.k = k;
   p.beta = beta;
   p.gcum = g_cumsum;
@@ -815,7 +837,7 @@ extern "C" int xk_solve_tril(const float* A, void* Ai, xk_dtype ai_dtype, int64_
   if (H <= 0) return XK_ERR_INVALID;
   if (!is_float_dtype(ai_dtype)) return XK_ERR_UNSUPPORTED;
   if (N == 0 || total_tokens == 0) return XK_OK;
-  if (!A || !Ai || !cu_seqlens || !aligned(A, 16)) return XK_ERR_INVALID;
+  if (!A || !Ai || !cu_seqlens || !aligned(A, 16) || !aligned(Ai, 16)) return XK_ERR_INVALID;
   p.A = A;
   p.Ai = Ai;
   p.H = static_cast<int>(H);
