@@ -1,0 +1,64 @@
+"""Committed golden vectors (tests/golden/golden_vectors.safetensors).
+
+CPU: the oracle, run on the stored inputs, still gives the stored outputs,
+and the seeded inputs regenerate exactly.  GPU: every HIP op, run through
+the C-ABI on the stored inputs, matches the stored outputs at the parity
+tolerances each case states.
+"""
+import os
+import sys
+
+import pytest
+import torch
+from safetensors.torch import load_file
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+sys.path.insert(0, GOLDEN)
+from cases import CASES  # noqa: E402
+from make_golden import PATH, seed_of  # noqa: E402
+
+NAMES = sorted(CASES)
+
+
+@pytest.fixture(scope="module")
+def vectors():
+    return load_file(PATH)
+
+
+def _split(vectors, name):
+    inp = {k.split("/", 2)[2]: v for k, v in vectors.items() if k.startswith(f"{name}/in/")}
+    out = {k.split("/", 2)[2]: v for k, v in vectors.items() if k.startswith(f"{name}/out/")}
+    return inp, out
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_inputs_regenerate(vectors, name):
+    inp, _ = _split(vectors, name)
+    g = torch.Generator().manual_seed(seed_of(name))
+    fresh = CASES[name].inputs(g)
+    assert sorted(fresh) == sorted(inp)
+    for k, v in fresh.items():
+        assert v.dtype == inp[k].dtype and torch.equal(v, inp[k]), k
+
+
+@pytest.mark.parametrize("name", NAMES)
+def test_oracle_reproduces(vectors, name):
+    inp, out = _split(vectors, name)
+    got = CASES[name].oracle({k: v.clone() for k, v in inp.items()})
+    assert sorted(got) == sorted(out)
+    for k, v in got.items():
+        assert v.dtype == out[k].dtype, k
+        torch.testing.assert_close(v, out[k], rtol=1e-5, atol=1e-6, msg=f"{name}/{k}")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", NAMES)
+def test_gpu_matches_golden(vectors, dev, name):
+    inp, out = _split(vectors, name)
+    c = CASES[name]
+    print(f"golden case {name}", flush=True)
+    got = c.gpu({k: v.to(dev) for k, v in inp.items()})
+    assert sorted(got) == sorted(out)
+    for k, v in got.items():
+        torch.testing.assert_close(v.float().cpu(), out[k].float(), **c.tol[k],
+                                   msg=f"{name}/{k}")

@@ -90,11 +90,12 @@ def test_solve_tril(dev, cu_list, out_dtype):
 
 
 @pytest.mark.parametrize("cu_list", CU_CASES)
-def test_recompute_w_u(dev, cu_list):
+@pytest.mark.parametrize("ai_dtype", [torch.bfloat16, torch.float32])
+def test_recompute_w_u(dev, cu_list, ai_dtype):
     from torch_npu_ops_amd import ops
     _, k, v, g, beta, _, cu = _inputs(cu_list)
     gc = og.chunk_local_cumsum(g.unsqueeze(0), cu)[0]
-    Ai = og.solve_tril(og.chunk_scaled_dot_kkt(k, beta, gc, cu), cu).bfloat16()
+    Ai = og.solve_tril(og.chunk_scaled_dot_kkt(k, beta, gc, cu), cu).to(ai_dtype)
     w, u = ops.npu_recompute_w_u_fwd(_b(k, dev), _b(v, dev), _b(beta, dev), _b(gc, dev),
                                      _b(Ai, dev), cu.to(dev))
     rw, ru = og.recompute_w_u(k, v, beta, gc, Ai, cu)
