@@ -293,6 +293,61 @@ class RopeCase(Case):
                 "full config 1 (256 tokens), fp32", 1.0)
 
 
+class RopePrefillCase(Case):
+    """Config 1's op at a prefill size, with cos/sin computed in registers
+    from positions: config 1 (256 tokens, 12.8 MB) is bounded by launch
+    latency, this shows the same kernel where HBM is the bound."""
+    name = "split_rmsnorm_rope_prefill"
+    config = ("split q/k RMSNorm + neox RoPE bf16 at prefill size: 16384 tokens, 32 q + "
+              "8 kv heads, head_dim 128, eps 1e-6, theta 1e6, cos/sin from int64 "
+              "positions U[0,4096) in registers")
+    kernel = "split_rmsnorm_rope_kernel"
+    T, HQ, HKV, HD = 16384, 32, 8, 128
+    # qkv in + q/k/v out (bf16) + positions (int64) + q/k weights + inv_freq
+    algo_bytes = T * (HQ + 2 * HKV) * HD * 2 * 2 + T * 8 + 2 * HD * 2 + HD // 2 * 4
+    CPU_T = 1024
+
+    def __init__(self):
+        g = torch.Generator().manual_seed(0)
+        hid = (self.HQ + 2 * self.HKV) * self.HD
+        self.qkv = _randn((self.T, hid), g, torch.bfloat16)
+        self.qw = _randn((self.HD,), g, torch.bfloat16, 0.1, 1.0)
+        self.kw = _randn((self.HD,), g, torch.bfloat16, 0.1, 1.0)
+        self.pos = torch.randint(0, 4096, (self.T,), generator=g)
+        i = torch.arange(0, self.HD, 2, dtype=torch.float64)
+        self.inv = (1.0 / (1e6 ** (i / self.HD))).to(torch.float32)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        qw, kw, inv = self.qw.to(dev), self.kw.to(dev), self.inv.to(dev)
+        qh, kvh = self.HQ * self.HD, self.HKV * self.HD
+        out = []
+        for _ in range(n):
+            qkv, pos = self.qkv.to(dev), self.pos.to(dev)
+            q = torch.empty(self.T, qh, device=dev, dtype=torch.bfloat16)
+            k = torch.empty(self.T, kvh, device=dev, dtype=torch.bfloat16)
+            v = torch.empty(self.T, kvh, device=dev, dtype=torch.bfloat16)
+
+            def run(qkv=qkv, pos=pos, q=q, k=k, v=v):
+                _ok(lib.xk_split_rmsnorm_rope(
+                    qkv.data_ptr(), qkv.stride(0), self.T, None, None, self.HD,
+                    pos.data_ptr(), _lib.XK_I64, inv.data_ptr(), q.data_ptr(),
+                    k.data_ptr(), v.data_ptr(), qw.data_ptr(), None, kw.data_ptr(), None,
+                    _lib.XK_BF16, qh, kvh, self.HD, 1e-6, _lib.XK_BF16, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import rope as orp
+        t = self.CPU_T
+        cos, sin = orp.neox_cos_sin(self.pos[:t], self.inv)
+        a = (self.qkv[:t], sin, cos, self.qw, self.kw, self.HQ * self.HD,
+             self.HKV * self.HD, self.HD, 1e-6)
+        return (lambda: orp.split_rmsnorm_rope(*a),
+                f"first {t} tokens, fp32 math incl. cos/sin rows", self.T / t)
+
+
 def varlen_lengths(n, total, lo, hi, gen):
     """n lengths ~ U{lo..hi}, repaired at seeded positions to sum to total."""
     lens = torch.randint(lo, hi + 1, (n,), generator=gen)
@@ -833,7 +888,8 @@ class L2NormCase(Case):
         return (lambda: on.l2norm_last_dim(x, 1e-6), "full shape, fp32 math on bf16 input", 1.0)
 
 
-CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, ConvPrefillCase,
+CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, RopePrefillCase,
+                             ConvPrefillCase,
                              ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase,
                              GdnChunkCase, GdnChunkStagedCase, GdnGatingCase,
                              GdnSigmoidGatingCase, GatedRmsNormCase, QkvzbaSplitCase,

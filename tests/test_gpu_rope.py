@@ -99,6 +99,38 @@ def test_head_dims_bias_and_aux_dtype(dev, hd, dtype, aux):
     _check(out0, ref0, dtype)
 
 
+# Wave-per-token kernel (positions mode at any size, table mode from 1024
+# tokens): 1027 tokens leave a partial last block; 6 q + 3 kv heads give the
+# teams of a wave unequal head counts.
+@pytest.mark.parametrize("hd,dtype,aux", [(128, torch.bfloat16, torch.bfloat16),
+                                          (64, torch.bfloat16, torch.float32),
+                                          (256, torch.float16, torch.float16),
+                                          (128, torch.float32, torch.float32)])
+@pytest.mark.parametrize("mode", ["positions", "table"])
+def test_token_kernel(dev, hd, dtype, aux, mode):
+    from torch_npu_ops_amd import ops
+    T, hq, hkv = 1027, 6, 3
+    qkv, qw, kw, pos, inv, cos, sin = _case(T, hq, hkv, hd, dtype, 11, aux=aux)
+    g = torch.Generator().manual_seed(12)
+    qb = torch.randn(hd, generator=g).to(aux)
+    kb = torch.randn(hd, generator=g).to(aux)
+    if mode == "positions":
+        # the kernel forms cos/sin in fp32, so the oracle gets the fp32 rows
+        cos, sin = orp.neox_cos_sin(pos, inv)
+    ref = orp.split_rmsnorm_rope(qkv, sin, cos, qw, kw, hq * hd, hkv * hd, hd, 1e-6,
+                                 q_bias=qb, k_bias=kb)
+    if mode == "positions":
+        out = ops.npu_split_rmsnorm_rope(qkv.to(dev), None, None, qw.to(dev), kw.to(dev),
+                                         hq * hd, hkv * hd, hd, 1e-6, q_bias=qb.to(dev),
+                                         k_bias=kb.to(dev), bias=True, positions=pos.to(dev),
+                                         inv_freq=inv.to(dev))
+    else:
+        out = ops.npu_split_rmsnorm_rope(qkv.to(dev), sin.to(dev), cos.to(dev), qw.to(dev),
+                                         kw.to(dev), hq * hd, hkv * hd, hd, 1e-6,
+                                         q_bias=qb.to(dev), k_bias=kb.to(dev), bias=True)
+    _check(out, ref, dtype)
+
+
 def test_single_token_and_empty(dev):
     from torch_npu_ops_amd import ops
     qkv, qw, kw, pos, inv, cos, sin = _case(1, 4, 4, 128, torch.bfloat16, 4)

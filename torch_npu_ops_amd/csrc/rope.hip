@@ -175,8 +175,131 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
   st_f32<T, kVec>(dst + kHalf + d0, o2);
 }
 
+// One wave per token.  The wave's 64 / kTeam teams take the token's heads
+// in turn (team t: heads t, t + teams, ...) with the lane layout of
+// split_rmsnorm_rope_kernel, so each lane forms its cos/sin (from the
+// position, or loaded) and its q/k weights once and reuses them for every
+// head of the token; computing sincosf per (token, head) made the
+// positions mode VALU-bound at prefill sizes.
+template <typename T, typename A, int HD, bool POS>
+__global__ void __launch_bounds__(256) split_rmsnorm_rope_tok_kernel(RopeParams p) {
+  constexpr int kHalf = HD / 2;
+  constexpr int kVec = (16 / sizeof(T)) < kHalf ? (16 / sizeof(T)) : kHalf;
+  constexpr int kTeam = kHalf / kVec;
+  constexpr int kTpw = kWave / kTeam;  // teams per wave
+  static_assert(kTeam >= 1 && kTeam <= kWave, "team must fit a wave");
+
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (tok >= p.T) return;  // whole wave
+  const int ln = threadIdx.x & 63;
+  const int team = ln / kTeam;
+  const int d0 = (ln % kTeam) * kVec;
+  using VT = Vec<T, kVec>;
+  using VA = Vec<A, kVec>;
+  const T* row = reinterpret_cast<const T*>(p.qkv) + tok * p.stride_row;
+
+  // cos / sin of the lane's dims d0.. and half + d0.. (equal in the
+  // positions mode, where the neox rows repeat).
+  constexpr int kCS = POS ? 1 : 2;
+  float c[kCS][kVec], sn[kCS][kVec];
+  if constexpr (POS) {
+    const float pos = p.pos_is_i64
+                          ? static_cast<float>(reinterpret_cast<const int64_t*>(p.pos)[tok])
+                          : static_cast<float>(reinterpret_cast<const int32_t*>(p.pos)[tok]);
+    float f[kVec];
+    ld_f32<float, kVec>(p.inv_freq + d0, f);
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) sincosf(pos * f[u], &sn[0][u], &c[0][u]);
+  } else {
+    const A* cs = reinterpret_cast<const A*>(p.cos) + tok * p.stride_sc;
+    const A* ss = reinterpret_cast<const A*>(p.sin) + tok * p.stride_sc;
+    ld_f32<A, kVec>(cs + d0, c[0]);
+    ld_f32<A, kVec>(cs + kHalf + d0, c[kCS - 1]);
+    ld_f32<A, kVec>(ss + d0, sn[0]);
+    ld_f32<A, kVec>(ss + kHalf + d0, sn[kCS - 1]);
+  }
+  // q and k weights (and biases; without one, the weight is read and
+  // multiplied by zero), kept in their storage type until used.
+  const A* qw = reinterpret_cast<const A*>(p.qw);
+  const A* kw = reinterpret_cast<const A*>(p.kw);
+  const A* qb = p.qb ? reinterpret_cast<const A*>(p.qb) : qw;
+  const A* kb = p.kb ? reinterpret_cast<const A*>(p.kb) : kw;
+  const float qbs = p.qb ? 1.f : 0.f, kbs = p.kb ? 1.f : 0.f;
+  const VA wq1 = *reinterpret_cast<const VA*>(qw + d0);
+  const VA wq2 = *reinterpret_cast<const VA*>(qw + kHalf + d0);
+  const VA wk1 = *reinterpret_cast<const VA*>(kw + d0);
+  const VA wk2 = *reinterpret_cast<const VA*>(kw + kHalf + d0);
+  const VA bq1 = *reinterpret_cast<const VA*>(qb + d0);
+  const VA bq2 = *reinterpret_cast<const VA*>(qb + kHalf + d0);
+  const VA bk1 = *reinterpret_cast<const VA*>(kb + d0);
+  const VA bk2 = *reinterpret_cast<const VA*>(kb + kHalf + d0);
+
+  const int nqk = p.hq + p.hkv;
+  auto src_of = [&](int h) {
+    const bool is_q = h < p.hq;
+    return row + (is_q ? 0 : p.q_hidden) + static_cast<int64_t>(is_q ? h : h - p.hq) * HD;
+  };
+  auto rope_head = [&](int h, const VT& xa, const VT& xb) {
+    const bool is_q = h < p.hq;
+    const int hh = is_q ? h : h - p.hq;
+    T* dst = reinterpret_cast<T*>(is_q ? p.q : p.k) +
+             tok * (is_q ? p.q_hidden : p.kv_hidden) + static_cast<int64_t>(hh) * HD;
+    float x1[kVec], x2[kVec];
+    vec_f32(xa, x1);
+    vec_f32(xb, x2);
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) ss = fmaf(x1[u], x1[u], fmaf(x2[u], x2[u], ss));
+    ss = group_sum<kTeam>(ss);
+    const float r = 1.0f / sqrtf(ss * (1.0f / HD) + p.eps);
+    const float bs = is_q ? qbs : kbs;
+    float o1[kVec], o2[kVec];
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      const float w1 = to_f32(is_q ? wq1.v[u] : wk1.v[u]);
+      const float w2 = to_f32(is_q ? wq2.v[u] : wk2.v[u]);
+      const float b1 = to_f32(is_q ? bq1.v[u] : bk1.v[u]) * bs;
+      const float b2 = to_f32(is_q ? bq2.v[u] : bk2.v[u]) * bs;
+      const float n1 = fmaf(x1[u] * r, w1, b1);
+      const float n2 = fmaf(x2[u] * r, w2, b2);
+      o1[u] = n1 * c[0][u] - n2 * sn[0][u];
+      o2[u] = n2 * c[kCS - 1][u] + n1 * sn[kCS - 1][u];
+    }
+    st_f32<T, kVec>(dst + d0, o1);
+    st_f32<T, kVec>(dst + kHalf + d0, o2);
+  };
+  for (int h = team; h < nqk; h += kTpw) {
+    const T* sa = src_of(h);
+    rope_head(h, ld_stream(reinterpret_cast<const VT*>(sa + d0)),
+              ld_stream(reinterpret_cast<const VT*>(sa + kHalf + d0)));
+  }
+  for (int h = team; h < p.hkv; h += kTpw) {  // v: copy through
+    const T* src = row + p.q_hidden + p.kv_hidden + static_cast<int64_t>(h) * HD;
+    T* dst = reinterpret_cast<T*>(p.v) + tok * p.kv_hidden + static_cast<int64_t>(h) * HD;
+    const VT a = ld_stream(reinterpret_cast<const VT*>(src + d0));
+    const VT c = ld_stream(reinterpret_cast<const VT*>(src + kHalf + d0));
+    st_stream(reinterpret_cast<VT*>(dst + d0), a);
+    st_stream(reinterpret_cast<VT*>(dst + kHalf + d0), c);
+  }
+}
+
+// Tokens from which table-mode calls use the wave-per-token kernel: below
+// it, one team per (token, head) gives the launch more waves to spread over
+// the 256 CUs.  The positions mode always uses it.
+constexpr int64_t kRopeTokKernelMin = 1024;
+
 template <typename T, typename A, int HD>
 int launch_rope(const RopeParams& p, hipStream_t s) {
+  if (p.pos) {
+    hipLaunchKernelGGL((split_rmsnorm_rope_tok_kernel<T, A, HD, true>), dim3(cdiv(p.T, 4)),
+                       dim3(256), 0, s, p);
+    return launch_status();
+  }
+  if (p.T >= kRopeTokKernelMin) {
+    hipLaunchKernelGGL((split_rmsnorm_rope_tok_kernel<T, A, HD, false>), dim3(cdiv(p.T, 4)),
+                       dim3(256), 0, s, p);
+    return launch_status();
+  }
   constexpr int kHalf = HD / 2;
   constexpr int kVec = (16 / sizeof(T)) < kHalf ? (16 / sizeof(T)) : kHalf;
   constexpr int kTeams = 256 / (kHalf / kVec);
