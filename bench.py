@@ -301,7 +301,7 @@ class RopePrefillCase(Case):
     config = ("split q/k RMSNorm + neox RoPE bf16 at prefill size: 16384 tokens, 32 q + "
               "8 kv heads, head_dim 128, eps 1e-6, theta 1e6, cos/sin from int64 "
               "positions U[0,4096) in registers")
-    kernel = "split_rmsnorm_rope_kernel"
+    kernel = "split_rmsnorm_rope_tok_kernel"
     T, HQ, HKV, HD = 16384, 32, 8, 128
     # qkv in + q/k/v out (bf16) + positions (int64) + q/k weights + inv_freq
     algo_bytes = T * (HQ + 2 * HKV) * HD * 2 * 2 + T * 8 + 2 * HD * 2 + HD // 2 * 4
