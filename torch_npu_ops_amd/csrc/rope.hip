@@ -363,6 +363,37 @@ __global__ void __launch_bounds__(256)
   *reinterpret_cast<VT*>(xp) = ov;
 }
 
+// One wave per token (vector path, rope_dim / VEC lanes per row dividing
+// the wave): each lane loads its sin/cos vectors once and rotates the same
+// slice of every head of the token, with a pass per 64 / lanes-per-row heads.
+template <typename T, typename A, int VEC, int LPR>
+__global__ void __launch_bounds__(256)
+    rope_inplace_tok_kernel(T* __restrict__ x, const A* __restrict__ sin,
+                            const A* __restrict__ cos, int64_t tokens, int head_num, int64_t sx,
+                            int64_t ssc, int64_t off) {
+  constexpr int kRpp = kWave / LPR;  // rows (heads) per pass
+  const int64_t tok = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (tok >= tokens) return;  // whole wave
+  const int ln = threadIdx.x & 63;
+  const int e0 = (ln % LPR) * VEC;
+  using VT = Vec<T, VEC>;
+  using VA = Vec<A, VEC>;
+  const VA sv = *reinterpret_cast<const VA*>(sin + tok * ssc + e0);
+  const VA cv = *reinterpret_cast<const VA*>(cos + tok * ssc + e0);
+  for (int h = ln / LPR; h < head_num; h += kRpp) {
+    T* xp = x + (tok * head_num + h) * sx + off + e0;
+    const VT xv = *reinterpret_cast<const VT*>(xp);
+    VT ov;
+#pragma unroll
+    for (int u = 0; u < VEC; u += 2) {
+      const float x0 = to_f32(xv.v[u]), x1 = to_f32(xv.v[u + 1]);
+      ov.v[u] = from_f32<T>(x0 * to_f32(cv.v[u]) - x1 * to_f32(sv.v[u]));
+      ov.v[u + 1] = from_f32<T>(x1 * to_f32(cv.v[u + 1]) + x0 * to_f32(sv.v[u + 1]));
+    }
+    *reinterpret_cast<VT*>(xp) = ov;
+  }
+}
+
 template <typename T, typename A>
 int launch_rope_inplace(void* x, const void* sin, const void* cos, int64_t rows, int head_num,
                         int64_t sx, int64_t ssc, int64_t hidden, int64_t rope_dim,
@@ -379,6 +410,13 @@ int launch_rope_inplace(void* x, const void* sin, const void* cos, int64_t rows,
   T* xp = static_cast<T*>(x);
   const A* sp = static_cast<const A*>(sin);
   const A* cp = static_cast<const A*>(cos);
+  // Whole tokens (rows = tokens x head_num) with 8 lanes per row.
+  if (vec && lanes == 8 && rows % head_num == 0) {
+    const int64_t tokens = rows / head_num;
+    hipLaunchKernelGGL((rope_inplace_tok_kernel<T, A, kV, 8>), dim3(cdiv(tokens, 4)), dim3(256), 0,
+                       s, xp, sp, cp, tokens, head_num, sx, ssc, off);
+    return launch_status();
+  }
   if (vec)
     hipLaunchKernelGGL((rope_inplace_kernel<T, A, kV>), grid, dim3(256), 0, s, xp, sp, cp, rows,
                        head_num, sx, ssc, off, lanes);
