@@ -99,8 +99,7 @@ def test_head_dims_bias_and_aux_dtype(dev, hd, dtype, aux):
     _check(out0, ref0, dtype)
 
 
-# Wave-per-token kernel (positions mode at any size, table mode from 1024
-# tokens): 1027 tokens leave a partial last block; 6 q + 3 kv heads give the
+# Wave-per-token kernel (from 1024 tokens): 1027 tokens leave a partial last block; 6 q + 3 kv heads give the
 # teams of a wave unequal head counts.
 @pytest.mark.parametrize("hd,dtype,aux", [(128, torch.bfloat16, torch.bfloat16),
                                           (64, torch.bfloat16, torch.float32),

@@ -283,14 +283,14 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_tok_kernel(RopeParams 
   }
 }
 
-// Tokens from which table-mode calls use the wave-per-token kernel: below
-// it, one team per (token, head) gives the launch more waves to spread over
-// the 256 CUs.  The positions mode always uses it.
+// Tokens from which the wave-per-token kernel is used: below it, one team
+// per (token, head) gives the launch more waves to spread over the 256 CUs
+// (at 256 tokens: 5.3 us against 12.7 us).
 constexpr int64_t kRopeTokKernelMin = 1024;
 
 template <typename T, typename A, int HD>
 int launch_rope(const RopeParams& p, hipStream_t s) {
-  if (p.pos) {
+  if (p.pos && p.T >= kRopeTokKernelMin) {
     hipLaunchKernelGGL((split_rmsnorm_rope_tok_kernel<T, A, HD, true>), dim3(cdiv(p.T, 4)),
                        dim3(256), 0, s, p);
     return launch_status();
