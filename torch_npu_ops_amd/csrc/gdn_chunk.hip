@@ -48,11 +48,18 @@ using namespace gdn;
 
 constexpr int kBVMax = 64;  // most V columns per P2 block (32 or 64)
 constexpr int kTh = 256;  // threads per block
-// Per-(chunk, head) record: ai_hi, ai_lo, aq (bf16 [64][64] each), then the
-// per-token factors (fp32 [5][64]: cq, ck, b, ed, exp(gc_last)).
-constexpr int kMat = kC * kC * 2;
-constexpr int kRec = 3 * kMat + 5 * kC * 4;  // 25856 = 101 * 256
+// Per-(chunk, head) record: ai_hi, ai_lo, aq, then the per-token factors
+// (fp32 [5][64]: cq, ck, b, ed, exp(gc_last)).  The three matrices are lower
+// triangular, so their zero upper-right 32 x 32 block is not stored: rows
+// 0..31 hold columns 0..31 (32 per row), rows 32..63 all 64 (tri_off).
+constexpr int kMat = (32 * 32 + 32 * 64) * 2;  // bf16 bytes per matrix
+constexpr int kRec = 3 * kMat + 5 * kC * 4;    // 19712 = 77 * 256
 static_assert(kRec % 256 == 0, "records stay 256-byte aligned");
+
+// Element offset of (row, col) in a stored triangle (col < 32 for row < 32).
+__device__ __forceinline__ int tri_off(int row, int col) {
+  return row < 32 ? row * 32 + col : 1024 + (row - 32) * 64 + col;
+}
 // Padded rows of a sequence's last chunk store their (unused) outputs here,
 // so that every store in the chunk loop is unconditional: gfx9 counts loads
 // and stores in one in-order counter, and a store that only some paths
@@ -207,16 +214,17 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   __bf16* ail = reinterpret_cast<__bf16*>(rec + kMat);
   __bf16* aqp = reinterpret_cast<__bf16*>(rec + 2 * kMat);
   float* sc = reinterpret_cast<float*>(rec + 3 * kMat);
-  // Ai as hi and lo bf16 rows.  Store j covers rows 8j .. 8j + 7, one
-  // contiguous KB (lane: row 8j + lane / 8, columns 8 (lane % 8) .. + 7), so
-  // every store instruction writes whole cache lines.
-  const int sr = lane >> 3, scol = (lane & 7) * 8;
+  // Ai as hi and lo bf16 triangles.  Store j writes stored elements
+  // 512 j .. 512 j + 511, one contiguous KB (lane: 8 consecutive elements of
+  // one row), so every store instruction writes whole cache lines.
+  auto tri_row = [&](int j) { return j < 2 ? 16 * j + (lane >> 2) : 8 * j + 16 + (lane >> 3); };
+  auto tri_col = [&](int j) { return j < 2 ? (lane & 3) * 8 : (lane & 7) * 8; };
 #pragma unroll
-  for (int j = 0; j < kC / 8; ++j) {
+  for (int j = 0; j < 6; ++j) {
     bf8_t h, l;
-    split8(&X[8 * j + sr][scol], h, l);
-    *reinterpret_cast<bf8_t*>(aih + (8 * j + sr) * kC + scol) = h;
-    *reinterpret_cast<bf8_t*>(ail + (8 * j + sr) * kC + scol) = l;
+    split8(&X[tri_row(j)][tri_col(j)], h, l);
+    *reinterpret_cast<bf8_t*>(aih + 512 * j + 8 * lane) = h;
+    *reinterpret_cast<bf8_t*>(ail + 512 * j + 8 * lane) = l;
   }
   __builtin_amdgcn_wave_barrier();
 
@@ -241,11 +249,11 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
     }
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
-  for (int j = 0; j < kC / 8; ++j) {
+  for (int j = 0; j < 6; ++j) {
     bf8_t h;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = static_cast<__bf16>(X[8 * j + sr][scol + e]);
-    *reinterpret_cast<bf8_t*>(aqp + (8 * j + sr) * kC + scol) = h;
+    for (int e = 0; e < 8; ++e) h[e] = static_cast<__bf16>(X[tri_row(j)][tri_col(j) + e]);
+    *reinterpret_cast<bf8_t*>(aqp + 512 * j + 8 * lane) = h;
   }
 
   // Per-token factors (lane = token); rows >= L are zero.
@@ -337,9 +345,13 @@ __device__ __forceinline__ void load_inv(const ChunkParams& p, InvOps& ops, int6
   const __bf16* aih = reinterpret_cast<const __bf16*>(rec);
   const __bf16* ail = reinterpret_cast<const __bf16*>(rec + kMat);
   const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
+  // Rows 0..31 have no stored columns 32..63 (zero): their kk = 1 operand
+  // re-reads the kk = 0 one, keeping every load unconditional, and is never
+  // multiplied (the Vn product skips it).
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
-    const int off = (wid * 16 + l15) * kC + kk * 32 + 8 * lg;
+    const int row = wid * 16 + l15;
+    const int off = tri_off(row, (row < 32 ? 0 : kk * 32) + 8 * lg);
     ops.aiH[kk] = *reinterpret_cast<const bf8_t*>(aih + off);
     ops.aiL[kk] = *reinterpret_cast<const bf8_t*>(ail + off);
   }
@@ -360,8 +372,10 @@ __device__ __forceinline__ void load_out(const ChunkParams& p, OutOps<K / 32>& o
   const __bf16* aqp = reinterpret_cast<const __bf16*>(rec + 2 * kMat);
   const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + (wid * 16 + l15) * kC + kk * 32 + 8 * lg);
+  for (int kk = 0; kk < 2; ++kk) {
+    const int row = wid * 16 + l15;  // rows 0..31: kk = 1 as for Ai
+    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + tri_off(row, (row < 32 ? 0 : kk * 32) + 8 * lg));
+  }
   ops.cq = sc[0 * kC + wid * 16 + l15];
 }
 
@@ -491,6 +505,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       vn[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
+        if (kk * 32 > wid * 16 + 15) continue;  // zero block of Ai (not stored)
         const bf8_t rh = *reinterpret_cast<const bf8_t*>(&sm.rt[0][nj * 16 + l15][kk * 32 + 8 * lg]);
         const bf8_t rl = *reinterpret_cast<const bf8_t*>(&sm.rt[1][nj * 16 + l15][kk * 32 + 8 * lg]);
         vn[nj] = mfma_split3(inv.aiH[kk], inv.aiL[kk], rh, rl, vn[nj]);
