@@ -153,19 +153,13 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   constexpr int KK = K / 32;
   const int64_t rs = static_cast<int64_t>(p.H) * K;
 
-  // K rows of the chunk as MFMA operands (A and B^T read the same rows),
-  // and the Q rows, all issued up front so the wave pays one load latency.
-  bf8_t kop[4][KK], qop[4][KK];
+  // K rows of the chunk as MFMA operands (A and B^T read the same rows).
+  bf8_t kop[4][KK];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
       kop[mi][kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qop[mi][kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
   // Per-token g (inclusive scan within the chunk) and beta; padded rows 0
   // (loads clamped to row L-1, then selected away).
   const int lt = min(lane, L - 1);
@@ -184,7 +178,6 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   // (row mi*16 + l15; the four lg lanes hold its four 32-wide pieces), or 1
   // without the in-op l2norm.
   row_scales<KK>(kop, rkv, p.l2norm);
-  row_scales<KK>(qop, rqv, p.l2norm);
   __builtin_amdgcn_wave_barrier();
 
   // M = strict_tril(b_i r_i r_j (k_i . k_j) exp(gc_i - gc_j)) into X (the
@@ -226,6 +219,17 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
     *reinterpret_cast<bf8_t*>(aih + 512 * j + 8 * lane) = h;
     *reinterpret_cast<bf8_t*>(ail + 512 * j + 8 * lane) = l;
   }
+  __builtin_amdgcn_wave_barrier();
+
+  // Q rows, loaded only now so that they are not live (64 registers)
+  // through the inverse.
+  bf8_t qop[4][KK];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      qop[mi][kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
+  row_scales<KK>(qop, rqv, p.l2norm);
   __builtin_amdgcn_wave_barrier();
 
   // Aq = scale * tril(r_q r_k (q k^T) exp(gc_i - gc_j)), rows < L.
