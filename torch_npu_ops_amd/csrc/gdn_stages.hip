@@ -437,6 +437,12 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
   const int64_t krow = static_cast<int64_t>(p.Hg) * K;
   const int64_t wrow = static_cast<int64_t>(p.H) * K;
   const bf8_t sel[2] = {select_op(0), select_op(1)};
+  // B operand picking, for output column n, slot 8 (n / 4) + n % 4: the first
+  // four slots of each lane group, i.e. the rows of one 16-row result tile.
+  bf8_t sel4;
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    sel4[e] = static_cast<__bf16>(lg == (l15 >> 2) && e == (l15 & 3) ? 1.0f : 0.0f);
   auto load_ops = [&](FwdHOps<KK>& o, int64_t ci) {
     const int64_t s = bos + ci * kC;
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
@@ -459,23 +465,43 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
     const int64_t cidx = c0 + ci;
     load_ops(nxt, min(ci + 1, nch - 1));
-    // Snapshot of the state entering this chunk, and its bf16 hi / lo copy.
+    // Snapshot of the state entering this chunk (bf16, the hi part), and its
+    // bf16 hi / lo copy.
     bf16* hdst = reinterpret_cast<bf16*>(p.h) + (cidx * p.H + h) * static_cast<int64_t>(K) * V;
+    Vec<__bf16, 4> shi[M2][2];
 #pragma unroll
     for (int m2 = 0; m2 < M2; ++m2)
 #pragma unroll
       for (int nj = 0; nj < 2; ++nj) {
-        Vec<__bf16, 4> hi, lo;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kr = wid * (K / 4) + m2 * 16 + 4 * lg + i;
-          hdst[static_cast<int64_t>(kr) * V + v0 + nj * 16 + l15] = from_f32<bf16>(sreg[m2][nj][i]);
-        }
-        split4(sreg[m2][nj], hi, lo);
+        Vec<__bf16, 4> lo;
+        split4(sreg[m2][nj], shi[m2][nj], lo);
         const int k0 = wid * (K / 4) + m2 * 16 + 4 * lg;
-        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][nj * 16 + l15][k0]) = hi;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][nj * 16 + l15][k0]) = shi[m2][nj];
         *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[1][nj * 16 + l15][k0]) = lo;
       }
+    // The snapshot is stored row-major (V fastest) as 8-byte vectors: the
+    // lane's two key tiles of column nj form an A operand (row = column
+    // v0 + 16 nj + l15, key slots), and select_op MFMAs (exact) hand each
+    // lane 4 consecutive columns of one key, kappa below.
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) {
+      bf8_t a;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = shi[0][nj].v[i];
+        a[4 + i] = shi[1][nj].v[i];
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const f4_t t = mfma16(a, sel[hh], f4_t{0.f, 0.f, 0.f, 0.f});
+        const int r = l15 + 16 * hh, g = r >> 3, e = r & 7;
+        const int kr = wid * (K / 4) + (e < 4 ? 4 * g + e : 16 + 4 * g + e - 4);
+        Vec<bf16, 4> o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.v[i] = static_cast<bf16>(t[i]);
+        *reinterpret_cast<Vec<bf16, 4>*>(hdst + static_cast<int64_t>(kr) * V + v0 + nj * 16 + 4 * lg) = o;
+      }
+    }
     store_kt<K, kLt>(sm.kt, cur.ka, sel);
     if (tid < kC) sm.gc[tid] = cur.gct;
     __syncthreads();
@@ -496,17 +522,28 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
       const f4_t uc = mfma16(cur.ua, sel[nj], f4_t{0.f, 0.f, 0.f, 0.f});
       Vec<__bf16, 4> dh, dl;
       f4_t d;
+      bf8_t vb = {};  // v_new (bf16) of this tile as an A operand, slots 0..3
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = wid * 16 + 4 * lg + i;
         const float vn = uc[i] - ws[nj][i];
-        // Rows >= L repeat row L-1 (their operands are clamped to it), so
-        // storing them at row L-1 rewrites the same value.
-        if (p.vnew)
-          reinterpret_cast<bf16*>(p.vnew)[((s + min(row, L - 1)) * p.H + h) * static_cast<int64_t>(V) +
-                                          v0 + nj * 16 + l15] = from_f32<bf16>(vn);
+        vb[i] = static_cast<__bf16>(vn);
         const float dec = row < L ? (p.gcum ? safe_exp(gl - sm.gc[row]) : 1.f) : 0.f;
         d[i] = vn * dec;
+      }
+      if (p.vnew) {
+        // Transposed by one MFMA so a lane holds 4 consecutive columns of
+        // token 16 wid + l15 (an 8-byte store).  Rows >= L repeat row L-1
+        // (their operands are clamped to it), so storing them at row L-1
+        // rewrites the same values.
+        const f4_t t = mfma16(vb, sel4, f4_t{0.f, 0.f, 0.f, 0.f});
+        const int row = wid * 16 + l15;
+        Vec<bf16, 4> o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o.v[i] = static_cast<bf16>(t[i]);
+        *reinterpret_cast<Vec<bf16, 4>*>(reinterpret_cast<bf16*>(p.vnew) +
+                                         ((s + min(row, L - 1)) * p.H + h) * static_cast<int64_t>(V) +
+                                         v0 + nj * 16 + 4 * lg) = o;
       }
       split4(d, dh, dl);
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = dh;
