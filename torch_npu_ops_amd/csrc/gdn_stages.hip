@@ -647,37 +647,42 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
   const bf8_t sel[2] = {select_op(0), select_op(1)};
   const f4_t zero = {0.f, 0.f, 0.f, 0.f};
 
+  // Every global operand is loaded before its first use: h and v_new rows
+  // for the transposes, then q and the key tiles of Aq, which stay in flight
+  // across the barrier.
   // h_c rows 32w .. 32w + 31 -> ht (transposed).
   const bf16* hsrc = reinterpret_cast<const bf16*>(p.h) + (c * p.H + h) * static_cast<int64_t>(K) * V;
+  bf8_t ha[2][V / 32];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int kk = 0; kk < V / 32; ++kk)
+      ha[mt][kk] = *reinterpret_cast<const bf8_t*>(hsrc + (wid * 32 + mt * 16 + l15) * V + kk * 32 + 8 * lg);
+  const int t = wid * 16 + l15;
+  const bf16* vsrc = reinterpret_cast<const bf16*>(p.v) +
+                     ((s + min(t, L - 1)) * p.H + h) * static_cast<int64_t>(V);
+  bf8_t va[V / 32];
+#pragma unroll
+  for (int kk = 0; kk < V / 32; ++kk) va[kk] = *reinterpret_cast<const bf8_t*>(vsrc + kk * 32 + 8 * lg);
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
     const int k0 = wid * 32 + mt * 16;
-    bf8_t a[V / 32];
-#pragma unroll
-    for (int kk = 0; kk < V / 32; ++kk)
-      a[kk] = *reinterpret_cast<const bf8_t*>(hsrc + (k0 + l15) * V + kk * 32 + 8 * lg);
 #pragma unroll
     for (int kk = 0; kk < V / 32; ++kk)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
-        const f4_t t = mfma16(a[kk], sel[hh], zero);
+        const f4_t tt = mfma16(ha[mt][kk], sel[hh], zero);
         Vec<__bf16, 4> b;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(t[i]);
+        for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(tt[i]);
         *reinterpret_cast<Vec<__bf16, 4>*>(&sm.ht[kk * 32 + hh * 16 + l15][k0 + 4 * lg]) = b;
       }
   }
   // v_new rows (tokens) 16w .. 16w + 15 -> vt (transposed), rows >= L zero.
   {
-    const int t = wid * 16 + l15;
-    const bf16* vsrc = reinterpret_cast<const bf16*>(p.v) +
-                       ((s + min(t, L - 1)) * p.H + h) * static_cast<int64_t>(V);
     bf8_t a[V / 32];
 #pragma unroll
-    for (int kk = 0; kk < V / 32; ++kk) {
-      a[kk] = *reinterpret_cast<const bf8_t*>(vsrc + kk * 32 + 8 * lg);
-      if (t >= L) a[kk] = bf8_t{};
-    }
+    for (int kk = 0; kk < V / 32; ++kk) a[kk] = t < L ? va[kk] : bf8_t{};
 #pragma unroll
     for (int kk = 0; kk < V / 32; ++kk)
 #pragma unroll
@@ -690,14 +695,19 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
       }
   }
   if (tid < kC) sm.gc[tid] = p.gcum ? p.gcum[(s + min(tid, L - 1)) * p.H + h] : 0.f;
-  __syncthreads();
-
   const int64_t qrow = static_cast<int64_t>(p.Hg) * K;
   const int tq = wid * 16 + l15;  // this lane's output token
-  bf8_t qa[KK];
+  bf8_t qa[KK], ka[4][KK];
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
     qa[kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, qrow, wid * 16, kk);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      ka[j][kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, qrow, j * 16, kk);
+  __syncthreads();
+
   const float gq = sm.gc[tq];
 
   // Aq^T tiles (key tokens 16j + 4lg + i, query token tq), j <= w.
@@ -707,9 +717,7 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
     at[j] = zero;
     if (j <= wid) {
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        at[j] = mfma16(load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, qrow, j * 16, kk),
-                       qa[kk], at[j]);
+      for (int kk = 0; kk < KK; ++kk) at[j] = mfma16(ka[j][kk], qa[kk], at[j]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int tk = j * 16 + 4 * lg + i;
