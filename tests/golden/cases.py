@@ -291,3 +291,61 @@ class QkvzbaSplit:
         from torch_npu_ops_amd import ops
         qkv, z, b, a = ops.npu_fused_qkvzba_split_reshape_cat(t["qkvz"], t["ba"], 2, 4, 32, 32)
         return dict(mixed_qkv=qkv, z=z, b=b, a=a)
+
+
+@case("gdn_stages")
+class GdnStages:
+    """The chunked pipeline stage by stage (cumsum, K K^T, solve_tril,
+    recompute_w_u, fwd_h, fwd_o), 3 sequences (1, 64 and 85 tokens), 1 qk /
+    2 v heads of 128.  Each stage's inputs are the oracle's outputs of the
+    stages before it (stored), so every stage kernel is checked on its own."""
+    tol = dict(gc=dict(rtol=1e-5, atol=1e-5), A=F32, Ai=STATE, w=BF16, u=BF16, h=BF16, vnew=BF16,
+               ht=STATE, o=BF16)
+
+    def inputs(self, g):
+        return dict(q=_bf((150, 1, 128), g), k=_bf((150, 1, 128), g), v=_bf((150, 2, 128), g),
+                    gate=F.logsigmoid(torch.randn(150, 2, generator=g)),
+                    beta=torch.sigmoid(torch.randn(150, 2, generator=g)).bfloat16(),
+                    h0=torch.randn(3, 2, 128, 128, generator=g) * 0.1,
+                    cu=torch.tensor([0, 1, 65, 150], dtype=torch.int32))
+
+    def oracle(self, t):
+        from oracle import gdn as og
+        k = og.l2norm(t["k"].float()).bfloat16()
+        q = og.l2norm(t["q"].float()).bfloat16()
+        cu = t["cu"]
+        gc = og.chunk_local_cumsum(t["gate"].unsqueeze(0), cu)[0]
+        A = og.chunk_scaled_dot_kkt(k, t["beta"], gc, cu)
+        Ai = og.solve_tril(A, cu)
+        w, u = og.recompute_w_u(k, t["v"], t["beta"], gc, Ai, cu)
+        w, u = w.bfloat16(), u.bfloat16()
+        h, vnew, ht = og.chunk_fwd_h(k, w, u, gc, t["h0"], cu)
+        o = og.chunk_fwd_o(q, k, vnew.bfloat16(), h.bfloat16(), gc, 0.0883883, cu)
+        # h and v_new are bf16 on the GPU side (the reference's stage dtypes)
+        return dict(gc=gc, A=A, Ai=Ai, w=w.float(), u=u.float(), h=h.bfloat16(),
+                    vnew=vnew.bfloat16(), ht=ht, o=o)
+
+    def gpu_with_golden(self, t, out, dev):
+        from torch_npu_ops_amd import ops
+        from oracle import gdn as og
+
+        def b(x):
+            return x.unsqueeze(0).to(dev)
+        k = og.l2norm(t["k"].float()).bfloat16()
+        q = og.l2norm(t["q"].float()).bfloat16()
+        cu = t["cu"].to(dev)
+        got = {}
+        got["gc"] = ops.npu_chunk_local_cumsum(b(t["gate"]), 64, cu)[0]
+        got["A"] = ops.npu_chunk_scaled_dot_kkt_fwd(b(k), b(t["beta"]), b(out["gc"]), 64, cu)[0]
+        got["Ai"] = ops.npu_solve_tril(b(out["A"]), 64, cu)[0]
+        w, u = ops.npu_recompute_w_u_fwd(b(k), b(t["v"]), b(t["beta"]), b(out["gc"]),
+                                         b(out["Ai"]), cu)
+        got["w"], got["u"] = w[0], u[0]
+        h, vnew, ht = ops.npu_chunk_gated_delta_rule_fwd_h(
+            b(k), b(out["w"].bfloat16()), b(out["u"].bfloat16()), b(out["gc"]), t["h0"].to(dev),
+            True, 64, True, cu)
+        got["h"], got["vnew"], got["ht"] = h[0], vnew[0, :150], ht
+        got["o"] = ops.npu_chunk_fwd_o(b(q), b(k), b(out["vnew"].bfloat16()),
+                                       out["h"].bfloat16().unsqueeze(0).to(dev), b(out["gc"]),
+                                       0.0883883, 64, cu)[0, :150]
+        return got

@@ -57,7 +57,10 @@ def test_gpu_matches_golden(vectors, dev, name):
     inp, out = _split(vectors, name)
     c = CASES[name]
     print(f"golden case {name}", flush=True)
-    got = c.gpu({k: v.to(dev) for k, v in inp.items()})
+    if hasattr(c, "gpu_with_golden"):  # stages fed with the stored oracle outputs
+        got = c.gpu_with_golden(inp, out, dev)
+    else:
+        got = c.gpu({k: v.to(dev) for k, v in inp.items()})
     assert sorted(got) == sorted(out)
     for k, v in got.items():
         torch.testing.assert_close(v.float().cpu(), out[k].float(), **c.tol[k],
