@@ -161,6 +161,8 @@ def test_rope_inplace_reference_cases(dev, batch, head):
     ((7, 4, 128), 128, torch.float32, torch.float32),    # whole row rotated
     ((9, 3, 96), 32, torch.float16, torch.float32),      # fp32 sin / cos
     ((5, 2, 40), 6, torch.bfloat16, torch.bfloat16),     # 3 pairs: pair path
+    ((6, 5, 64), 32, torch.float32, torch.float32),      # wave per token, fp32
+    ((10, 3, 128), 64, torch.float16, torch.float32),    # wave per token, fp32 sin / cos
 ])
 def test_rope_inplace_shapes(dev, shape, rope_dim, dtype, sdtype):
     _check_rope_inplace(dev, shape, rope_dim, dtype, sdtype, 11)
