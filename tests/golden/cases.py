@@ -16,7 +16,7 @@ import torch.nn.functional as F
 BF16 = dict(rtol=1.6e-2, atol=1e-2)   # bf16 outputs against fp32 references
 STAT = dict(rtol=1e-4, atol=1e-5)     # fp32 norm statistics
 F32 = dict(rtol=1e-4, atol=1e-4)      # fp32 outputs of fp32 math
-STATE = dict(rtol=1e-3, atol=1e-3)    # fp32 GDN states
+STATE = dict(rtol=1e-3, atol_per_rms=1e-3)  # fp32 GDN states: atol = 1e-3 * RMS(reference)
 EXACT = dict(rtol=0.0, atol=0.0)      # permutations, state shifts
 
 CASES = {}
@@ -205,7 +205,7 @@ class ConvVarlen:
 class GdnRecurrent:
     """Recurrent gated delta rule, 3 sequences x 1 token, 2 qk / 4 v heads,
     head dims 64, in-kernel l2norm, states updated in place."""
-    tol = dict(o=BF16, state=dict(rtol=1e-3, atol=1e-4))
+    tol = dict(o=BF16, state=STATE)
 
     def inputs(self, g):
         return dict(q=_bf((3, 2, 64), g), k=_bf((3, 2, 64), g), v=_bf((3, 4, 64), g),
@@ -299,7 +299,7 @@ class GdnStages:
     recompute_w_u, fwd_h, fwd_o), 3 sequences (1, 64 and 85 tokens), 1 qk /
     2 v heads of 128.  Each stage's inputs are the oracle's outputs of the
     stages before it (stored), so every stage kernel is checked on its own."""
-    tol = dict(gc=dict(rtol=1e-5, atol=1e-5), A=F32, Ai=STATE, w=BF16, u=BF16, h=BF16, vnew=BF16,
+    tol = dict(gc=dict(rtol=1e-5, atol=1e-5), A=F32, Ai=dict(rtol=1e-3, atol=1e-3), w=BF16, u=BF16, h=BF16, vnew=BF16,
                ht=STATE, o=BF16)
 
     def inputs(self, g):

@@ -11,7 +11,7 @@ npu_fused_sigmoid_gating_delta_rule_update: the (batch, H, HV) list of
 test_fused_sigmoid_gating_delta_rule_update.py:225-249 (T = 1, K = V = 128,
 l2norm on), varlen multi-token sequences, negative and repeated state
 indices and K = V = 64.  Against the kernel-arithmetic oracle (float64):
-o (bf16) rtol 1.6e-2 / atol 1e-2, final states (fp32) rtol 1e-3 / atol 1e-4;
+o (bf16) rtol 1.6e-2 / atol 1e-2, final states (fp32) rtol 1e-3 with atol = 1e-3 x RMS(reference);
 against the reference CPU ref's rounding (ref_rounding=True) at that test's
 own tolerances (o rtol 5e-3 / atol 1e-2, state rtol 5e-2 / atol 2e-2).
 """
@@ -19,11 +19,11 @@ import pytest
 import torch
 
 from oracle import gating as og
+from state_tol import assert_state_close
 
 pytestmark = pytest.mark.gpu
 
 O_TOL = dict(rtol=1.6e-2, atol=1e-2)
-S_TOL = dict(rtol=1e-3, atol=1e-4)
 
 HEADS = (1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64)
 
@@ -127,7 +127,7 @@ def test_update_reference_cases(dev, batch, H, HV):
     o, st = _run_update(dev, *args)
     ro, rs = og.sigmoid_gating_delta_rule_update(*args)
     torch.testing.assert_close(o, ro.float(), **O_TOL)
-    torch.testing.assert_close(st, rs.float(), **S_TOL)
+    assert_state_close(st, rs.float())
     # the reference test's own comparison (its CPU ref rounds beta and q/k)
     fo, fs = og.sigmoid_gating_delta_rule_update(*args, ref_rounding=True)
     torch.testing.assert_close(o, fo.float(), rtol=0.005, atol=0.01)
@@ -148,7 +148,7 @@ def test_update_varlen_and_negative_slots(dev, l2norm):
     o, st = _run_update(dev, *args)
     ro, rs = og.sigmoid_gating_delta_rule_update(*args)
     torch.testing.assert_close(o, ro.float(), **O_TOL)
-    torch.testing.assert_close(st, rs.float(), **S_TOL)
+    assert_state_close(st, rs.float())
     assert torch.equal(st[0], state[0]) and torch.equal(st[1], state[1])
     assert torch.equal(st[4], state[4])
 
@@ -162,7 +162,7 @@ def test_update_head_dim_64_and_cpp_api(dev):
     o, st = _run_update(dev, *args, api="cpp")
     ro, rs = og.sigmoid_gating_delta_rule_update(*args)
     torch.testing.assert_close(o, ro.float(), **O_TOL)
-    torch.testing.assert_close(st, rs.float(), **S_TOL)
+    assert_state_close(st, rs.float())
 
 
 def test_update_rejects_bad_arguments(dev):

@@ -3,7 +3,7 @@ decode step (C-ABI via ops) against oracle/gdn.py (float64) and
 oracle/conv1d.py on identical seeded inputs.
 
 Tolerances: outputs (bf16) rtol 1.6e-2 / atol 1e-2; final states (fp32)
-rtol 1e-3 / atol 1e-4 (north-star state tolerance; the reference's own
+rtol 1e-3 with atol = 1e-3 x RMS(reference) (the reference's own
 test allows rtol 5e-2 / atol 1e-2, test_fused_recurrent_gated_delta_rule.py:
 743-748).  Conv states are copies and must match exactly.
 """
@@ -13,11 +13,11 @@ import torch.nn.functional as F
 
 from oracle import conv1d as oc
 from oracle import gdn as og
+from state_tol import assert_state_close
 
 pytestmark = pytest.mark.gpu
 
 O_TOL = dict(rtol=1.6e-2, atol=1e-2)
-S_TOL = dict(rtol=1e-3, atol=1e-4)
 
 
 def _inputs(N, T, H, HV, D, g_norm, seed, gdt=torch.float32):
@@ -58,7 +58,7 @@ def test_recurrent_reference_cases(dev, B, T, H, HV, D, scale, gn):
         cu.to(dev), idx.to(dev))
     assert fin.data_ptr() == st_d.data_ptr()
     torch.testing.assert_close(o[0].float().cpu(), ref_o.float(), **O_TOL)
-    torch.testing.assert_close(st_d.cpu(), ref_st.float(), **S_TOL)
+    assert_state_close(st_d.cpu(), ref_st.float())
 
 
 def test_recurrent_config5_unfused(dev):
@@ -82,7 +82,7 @@ def test_recurrent_config5_unfused(dev):
         g.unsqueeze(0).to(dev), beta.unsqueeze(0).to(dev), None, st_d, True,
         cu.to(dev), idx.to(dev))
     torch.testing.assert_close(o[0].float().cpu(), ref_o.float(), **O_TOL)
-    torch.testing.assert_close(st_d.cpu(), ref_st.float(), **S_TOL)
+    assert_state_close(st_d.cpu(), ref_st.float())
 
 
 @pytest.mark.parametrize("case", ["accepted_offsets", "tp4_local"])
@@ -108,7 +108,7 @@ def test_recurrent_spec_decoding(dev, case):
         g.unsqueeze(0).to(dev), beta.unsqueeze(0).to(dev), scale, st_d, True,
         cu.to(dev), idx.to(dev), acc.to(dev))
     torch.testing.assert_close(o[0].float().cpu(), ref_o.float(), **O_TOL)
-    torch.testing.assert_close(st_d.cpu(), ref_st.float(), **S_TOL)
+    assert_state_close(st_d.cpu(), ref_st.float())
 
 
 @pytest.mark.parametrize("K", [64, 128])
@@ -132,7 +132,7 @@ def test_recurrent_varlen_not_inplace(dev, K):
         cu.to(dev), None)
     torch.testing.assert_close(o[0].float().cpu(), ref_o.float(), **O_TOL)
     keep = [0, 2, 3]  # sequence 1 is empty: its final state is not written
-    torch.testing.assert_close(fin.cpu()[keep], ref_st.float()[keep], **S_TOL)
+    assert_state_close(fin.cpu()[keep], ref_st.float()[keep])
 
 
 def _fused_case(B, H, HV, seed, pad_rows=()):
@@ -176,4 +176,4 @@ def test_fused_conv_decode(dev, B, H, HV, pads):
                             ssm_state_indices=cidx.clamp(min=0).to(dev))
     torch.testing.assert_close(o[live].float().cpu(), ref_o.float(), **O_TOL)
     assert torch.equal(cs_d.cpu(), ref_cs.to(torch.bfloat16))
-    torch.testing.assert_close(st_d.cpu(), ref_st.float(), **S_TOL)
+    assert_state_close(st_d.cpu(), ref_st.float())

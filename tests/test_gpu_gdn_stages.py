@@ -2,9 +2,9 @@
 against the oracle's stage restatements (oracle/gdn.py, fp32) fed the same
 inputs, on varlen tables with empty, one-token and chunk-boundary sequences.
 
-Tolerances: fp32 stage outputs (g_cumsum, A, Ai, final state) rtol 1e-3 /
-atol 1e-3 (they differ from the oracle by summation order and the ~2^-16
-hi/lo-split products); bf16 outputs (w, u, h, v_new, o) rtol 1.6e-2 /
+Tolerances: fp32 stage outputs (g_cumsum, A, Ai) rtol 1e-3 / atol 1e-3
+(they differ from the oracle by summation order and the ~2^-16 hi/lo-split
+products); final states rtol 1e-3 with atol = 1e-3 x RMS(reference); bf16 outputs (w, u, h, v_new, o) rtol 1.6e-2 /
 atol 1e-2.  The whole staged pipeline carries the reference's bf16
 intermediates (Ai, w, u, h, v_new), so it is compared with the fp32 whole-op
 oracle at the reference test's own tolerance, 1e-2 / 1e-2 on o and 2e-2 on
@@ -15,6 +15,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import gdn as og
+from state_tol import assert_state_close
 
 pytestmark = pytest.mark.gpu
 
@@ -118,7 +119,7 @@ def test_fwd_h(dev, cu_list):
     torch.testing.assert_close(h[0].float().cpu(), rh, **O_TOL)
     T = cu_list[-1]
     torch.testing.assert_close(vnew[0, :T].float().cpu(), rv[:T], **O_TOL)
-    torch.testing.assert_close(fin.cpu(), rf, **F32_TOL)
+    assert_state_close(fin.cpu(), rf)
 
 
 def test_fwd_h_no_decay_no_state(dev):
@@ -132,7 +133,7 @@ def test_fwd_h_no_decay_no_state(dev):
     assert vnew is None
     rh, _, rf = og.chunk_fwd_h(k, w, u, None, None, cu)
     torch.testing.assert_close(h[0].float().cpu(), rh, **O_TOL)
-    torch.testing.assert_close(fin.cpu(), rf, **F32_TOL)
+    assert_state_close(fin.cpu(), rf)
 
 
 @pytest.mark.parametrize("cu_list", CU_CASES)

@@ -8,6 +8,7 @@ import torch
 import torch.nn.functional as F
 
 from oracle import gdn as og
+from state_tol import assert_state_close
 
 pytestmark = pytest.mark.gpu
 
@@ -109,7 +110,7 @@ def test_recurrent_paths_and_oracle(dev, xt):
     assert f2.data_ptr() == s2.data_ptr()  # in place, the reference's contract
     ro, rs = og.recurrent_gdn(q[0], k[0], v[0], gate[0], beta[0], 0.1, h0, cu, idx)
     torch.testing.assert_close(o2[0].float().cpu(), ro.float(), rtol=1.6e-2, atol=1e-2)
-    torch.testing.assert_close(s2.cpu(), rs.float(), rtol=1e-3, atol=1e-4)
+    assert_state_close(s2.cpu(), rs.float())
 
 
 def test_chunk_paths_and_oracle(dev, xt):
@@ -130,7 +131,7 @@ def test_chunk_paths_and_oracle(dev, xt):
     assert torch.equal(o1, o2) and torch.equal(f1, f2)
     ro, rs = og.chunk_gdn(q, k, v, gate, beta, None, h0, cu, use_qk_l2norm=True)
     torch.testing.assert_close(o2.float().cpu(), ro, rtol=1.6e-2, atol=1e-2)
-    torch.testing.assert_close(f2.cpu(), rs, rtol=1e-3, atol=1e-3)
+    assert_state_close(f2.cpu(), rs)
     # no final state requested: an undefined tensor comes back as None
     _, f3 = xt.npu_chunk_gated_delta_rule(*d, cu_seqlens=cu.to(dev))
     assert f3 is None
@@ -182,3 +183,75 @@ def test_gdn_conv_decode_paths(dev, xt):
     o1 = ops.gdn_conv_decode(x, c1, cw, gate, beta, s1, H, HV)
     o2 = xt.npu_gdn_conv_decode(x, c2, cw, gate, beta, s2, H, HV)
     assert torch.equal(o1, o2) and torch.equal(c1, c2) and torch.equal(s1, s2)
+
+
+def test_recurrent_default_arguments_normalise_like_the_reference(dev, xt):
+    # The reference binary always l2-normalises q/k, whatever
+    # use_qk_l2norm_in_kernel says (npu_triton_recurrent_gated_delta_rule.cpp:
+    # 216-238): a call with default arguments, and one passing False, both
+    # match the oracle with the normalisation on.
+    g = _g(9)
+    B, H, HV, D = 6, 2, 4, 128
+    q = torch.randn(1, B, H, D, generator=g).bfloat16()
+    k = torch.randn(1, B, H, D, generator=g).bfloat16()
+    v = torch.randn(1, B, HV, D, generator=g).bfloat16()
+    gate = F.logsigmoid(torch.randn(1, B, HV, generator=g))
+    beta = torch.sigmoid(torch.randn(1, B, HV, generator=g)).bfloat16()
+    h0 = torch.randn(B, HV, D, D, generator=g) * 0.05
+    cu = torch.arange(B + 1, dtype=torch.int32)
+    idx = torch.arange(B, dtype=torch.int32)
+    ro, rs = og.recurrent_gdn(q[0], k[0], v[0], gate[0], beta[0], D ** -0.5, h0, cu, idx,
+                              use_qk_l2norm=True)
+    d = [t.to(dev) for t in (q, k, v, gate, beta)]
+    for flag in (None, False):
+        st = h0.to(dev)
+        kw = {} if flag is None else dict(use_qk_l2norm_in_kernel=flag)
+        o, _ = xt.npu_fused_recurrent_gated_delta_rule(
+            *d, initial_state=st, cu_seqlens=cu.to(dev), ssm_state_indices=idx.to(dev), **kw)
+        torch.testing.assert_close(o[0].float().cpu(), ro.float(), rtol=1.6e-2, atol=1e-2)
+        assert_state_close(st.cpu(), rs.float())
+
+
+def test_conv_update_always_applies_silu_like_the_reference(dev, xt):
+    # npu_triton_causal_conv1d_update.cpp:38 ignores `activation`: SiLU is
+    # built into its kernel.  activation=False still returns the SiLU result.
+    from oracle import conv1d as oc
+    g = _g(10)
+    x = torch.randn(8, 256, generator=g).bfloat16()
+    st = torch.randn(8, 256, 3, generator=g).bfloat16()
+    w = (torch.randn(256, 4, generator=g) * 0.5).bfloat16()
+    idx = torch.arange(8, dtype=torch.int32)
+    ry, rst = oc.causal_conv1d_update(x, st, w, None, True, idx)
+    for act in (True, False):
+        sd = st.to(dev)
+        y = xt.npu_causal_conv1d_update(x.to(dev), sd, w.to(dev), act,
+                                        conv_state_indices=idx.to(dev))
+        torch.testing.assert_close(y.float().cpu(), ry.float(), rtol=1.6e-2, atol=1e-2)
+        assert torch.equal(sd.cpu(), rst.to(torch.bfloat16))
+
+
+def test_sigmoid_gating_update_always_normalises_like_the_reference(dev, xt):
+    # The reference wrapper never passes use_qk_l2norm_in_kernel to its
+    # kernel, built with the normalisation on: False gives the l2norm result.
+    from oracle import gating as ogt
+    g = _g(11)
+    N, H, HV, D = 4, 2, 4, 128
+    q = torch.randn(1, N, H, D, generator=g).bfloat16()
+    k = torch.randn(1, N, H, D, generator=g).bfloat16()
+    v = torch.randn(1, N, HV, D, generator=g).bfloat16()
+    a = torch.randn(1, N, HV, generator=g).bfloat16()
+    b = torch.randn(1, N, HV, generator=g).bfloat16()
+    A_log = torch.randn(HV, generator=g)
+    dt_bias = torch.randn(HV, generator=g)
+    h0 = torch.randn(N, HV, D, D, generator=g) * 0.05
+    idx = torch.arange(N, dtype=torch.int32)
+    cu = torch.arange(N + 1, dtype=torch.int32)
+    ro, rs = ogt.sigmoid_gating_delta_rule_update(A_log, a, dt_bias, q, k, v, b, h0, idx, cu,
+                                                  D ** -0.5, True)
+    st = h0.to(dev)
+    o = xt.npu_fused_sigmoid_gating_delta_rule_update(
+        A_log.to(dev), a.to(dev), dt_bias.to(dev), q.to(dev), k.to(dev), v.to(dev), b.to(dev),
+        st, idx.to(dev), cu.to(dev), use_qk_l2norm_in_kernel=False)
+    torch.testing.assert_close(o.float().cpu().reshape(ro.shape), ro.float(), rtol=1.6e-2,
+                               atol=1e-2)
+    assert_state_close(st.cpu(), rs.float())

@@ -163,3 +163,134 @@ def test_v2_prefill_rule_keeps_last_inputs():
     assert torch.equal(st_ref[1], torch.zeros(6, 3))
     assert torch.equal(st_pre[1][:, 1:], x[5:7].t()) and torch.equal(st_pre[1][:, 0], torch.zeros(6))
     assert torch.equal(st_pre[0], x[2:5].t())
+
+
+def golden_v2_spec_loop(x, state, w, bias, qsl, mql, acc, slots=None,
+                        activation=True):
+    """Per-element float64 restatement of the speculative-decoding branch of
+    causal_conv1d_update_ref_v2 (test_causal_conv1d_update_v2.py:290-335):
+    eff = W-1 + mql-1; run = eff - (mql - len); the window starts at column
+    off = accepted-1 of the input slot; when len < run the new state is
+    old[off+1 : off+1+keep] (keep = run - len) followed by the inputs, else
+    the last `run` inputs.  Indexing is written out column by column, with
+    no slicing shared with oracle/conv1d.py."""
+    x = x.astype(np.float64)
+    st = state.astype(np.float64).copy()
+    old = st.copy()
+    w = w.astype(np.float64)
+    bias = np.zeros(w.shape[0]) if bias is None else bias.astype(np.float64)
+    lines, D, S = st.shape
+    W = w.shape[1]
+    eff = (W - 1) + (mql - 1)
+    out = np.zeros_like(x)
+    for b in range(len(qsl) - 1):
+        start, end = qsl[b], qsl[b + 1]
+        ln = end - start
+        if ln <= 0:
+            continue
+        slot = b if slots is None else int(slots[b])
+        off = int(acc[b]) - 1
+        run = eff - (mql - ln)
+        assert run >= 1 and off >= 0 and off + W - 1 <= S
+        for f in range(D):
+            for t in range(ln):
+                acc_v = bias[f]
+                for j in range(W):
+                    # window position j of output t: history column off+t+j
+                    # while t+j < W-1, else input token t+j-(W-1)
+                    p = t + j
+                    if p < W - 1:
+                        val = old[slot, f, off + p]
+                    else:
+                        val = x[start + p - (W - 1), f]
+                    acc_v += w[f, j] * val
+                out[start + t, f] = acc_v
+            if ln >= run:
+                for d in range(run):
+                    st[slot, f, d] = x[start + ln - run + d, f]
+            else:
+                keep = run - ln
+                assert off + 1 + keep <= S  # the reference raises otherwise
+                for d in range(keep):
+                    st[slot, f, d] = old[slot, f, off + 1 + d]
+                for t in range(ln):
+                    st[slot, f, keep + t] = x[start + t, f]
+    if activation:
+        out = out / (1.0 + np.exp(-out))
+    return out, st
+
+
+def _spec_case(seed, W, lens, varlen=True):
+    g = torch.Generator().manual_seed(seed)
+    B = len(lens)
+    mql = max(lens)
+    S = (W - 1) + (mql - 1)
+    D = 12
+    qsl = [0]
+    for n in lens:
+        qsl.append(qsl[-1] + n)
+    x = torch.randn(qsl[-1], D, generator=g, dtype=torch.float64)
+    state = torch.randn(B + 1, D, S, generator=g, dtype=torch.float64)
+    w = torch.randn(D, W, generator=g, dtype=torch.float64)
+    bias = torch.randn(D, generator=g, dtype=torch.float64)
+    slots = torch.randperm(B + 1, generator=g)[:B].int()
+    acc = torch.tensor([1 + int(torch.randint(0, mql, (1,), generator=g)) for _ in lens],
+                       dtype=torch.int32)
+    return x, state, w, bias, torch.tensor(qsl, dtype=torch.int32), mql, acc, slots
+
+
+@pytest.mark.parametrize("W", [2, 3, 4, 5])
+@pytest.mark.parametrize("lens", [[3, 3, 3], [1, 4, 2, 4], [2, 1]])
+def test_v2_spec_oracle_matches_per_element_loop(W, lens):
+    x, state, w, bias, qsl, mql, acc, slots = _spec_case(10 * W + len(lens), W, lens)
+    out, st = oc.causal_conv1d_update_v2(
+        x, state, w, bias, True, slots, qsl, mql, num_accepted_tokens=acc,
+        dtype=torch.float64)
+    ref_out, ref_st = golden_v2_spec_loop(
+        x.numpy(), state.numpy(), w.numpy(), bias.numpy(), qsl.tolist(), mql,
+        acc.numpy(), slots.numpy())
+    np.testing.assert_allclose(out.numpy(), ref_out, rtol=1e-12, atol=1e-12)
+    np.testing.assert_array_equal(st.numpy(), ref_st)
+
+
+@pytest.mark.parametrize("W", [3, 4, 6])
+def test_v2_spec_identity_weight_closed_form(W):
+    # Weight e_{W-1}: out = silu(x) whatever the history; the new state is
+    # old[off+1 : off+1+keep] (keep = W-2 for every length) followed by the
+    # sequence's inputs; columns past run keep their old values.
+    lens = [3, 1, 2]
+    x, state, _, _, qsl, mql, acc, slots = _spec_case(W, W, lens)
+    D = x.shape[1]
+    w = torch.zeros(D, W, dtype=torch.float64)
+    w[:, -1] = 1
+    out, st = oc.causal_conv1d_update_v2(
+        x, state, w, None, True, slots, qsl, mql, num_accepted_tokens=acc,
+        dtype=torch.float64)
+    torch.testing.assert_close(out, F.silu(x), rtol=1e-15, atol=1e-15)
+    keep = W - 2
+    for b, n in enumerate(lens):
+        s, off = int(slots[b]), int(acc[b]) - 1
+        start = int(qsl[b])
+        expect = torch.cat([state[s, :, off + 1:off + 1 + keep], x[start:start + n].t()], 1)
+        assert torch.equal(st[s, :, :keep + n], expect)
+        assert torch.equal(st[s, :, keep + n:], state[s, :, keep + n:])
+    untouched = sorted(set(range(state.shape[0])) - set(slots.tolist()))
+    for s in untouched:
+        assert torch.equal(st[s], state[s])
+
+
+def test_v2_spec_first_tap_reads_accepted_column():
+    # Weight e_0, one token per sequence: the output is the state column
+    # off = accepted-1 (the oldest element of the window), pre-SiLU.
+    W, lens = 4, [1, 1, 1]
+    x, state, _, _, qsl, mql, _, slots = _spec_case(5, W, lens)
+    mql = 3  # state holds W-1 + mql-1 = 5 columns; accepted 1..3
+    state = torch.randn(4, x.shape[1], W - 1 + mql - 1, dtype=torch.float64)
+    acc = torch.tensor([1, 2, 3], dtype=torch.int32)
+    w = torch.zeros(x.shape[1], W, dtype=torch.float64)
+    w[:, 0] = 1
+    out, _ = oc.causal_conv1d_update_v2(
+        x, state, w, None, False, slots, qsl, mql, num_accepted_tokens=acc,
+        dtype=torch.float64)
+    for b in range(3):
+        assert torch.equal(out[b], state[int(slots[b]), :, int(acc[b]) - 1])

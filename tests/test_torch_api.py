@@ -75,3 +75,56 @@ def test_conv_update_query_start_loc_sentinel(xt):
                                       torch.zeros(8, 4),
                                       query_start_loc=torch.tensor([0, 1, 2]))
     assert out.shape == (1,) and out.item() == 0
+
+
+def test_chunk_initial_state_dtype_is_checked(xt):
+    # reference npu_triton_chunk_gated_delta_rule.cpp:574-579
+    q = torch.zeros(1, 8, 2, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="initial_state to be bfloat16 or float32"):
+        xt.npu_chunk_gated_delta_rule(q, q, q, torch.zeros(1, 8, 2), torch.zeros(1, 8, 2),
+                                      initial_state=torch.zeros(1, 2, 128, 128,
+                                                                dtype=torch.float16))
+
+
+def _conv_decode_args(ssm_dtype=torch.float32, conv_dtype=torch.bfloat16, ssm_shape=None):
+    B, H, HV, K = 2, 1, 2, 128
+    D = 2 * H * K + HV * K
+    x = torch.zeros(B, D, dtype=torch.bfloat16)
+    conv_state = torch.zeros(B, D, 3, dtype=conv_dtype)
+    w = torch.zeros(D, 4, dtype=torch.bfloat16)
+    g = torch.zeros(B, HV)
+    beta = torch.zeros(B, HV, dtype=torch.bfloat16)
+    ssm = torch.zeros(ssm_shape or (B, HV, K, K), dtype=ssm_dtype)
+    return x, conv_state, w, g, beta, ssm, H, HV
+
+
+@pytest.mark.parametrize("bad,match", [
+    (dict(ssm_dtype=torch.bfloat16), "ssm_state must be float32"),
+    (dict(ssm_shape=(2, 2, 128, 64)), "ssm_state must have shape"),
+    (dict(conv_dtype=torch.float32), "conv_state must have mixed_qkv's dtype"),
+])
+def test_gdn_conv_decode_rejects_bad_state_buffers(xt, bad, match):
+    # A state of another dtype or shape would be indexed past its end by the
+    # kernel; both the C++ drop-in and the Python mirror refuse it first.
+    from torch_npu_ops_amd import ops
+    args = _conv_decode_args(**bad)
+    with pytest.raises(RuntimeError, match=match):
+        xt.npu_gdn_conv_decode(*args)
+    with pytest.raises(ValueError, match=match):
+        ops.gdn_conv_decode(*args)
+
+
+def test_gdn_conv_decode_rejects_non_contiguous_state(xt):
+    from torch_npu_ops_amd import ops
+    x, cs, w, g, beta, _, H, HV = _conv_decode_args()
+    ssm = torch.zeros(2, HV, 128, 128).transpose(2, 3)
+    with pytest.raises(RuntimeError, match="contiguous within each slot"):
+        xt.npu_gdn_conv_decode(x, cs, w, g, beta, ssm, H, HV)
+    with pytest.raises(ValueError, match="contiguous within each slot"):
+        ops.gdn_conv_decode(x, cs, w, g, beta, ssm, H, HV)
+
+
+def test_operation_base_keeps_npubin_path_parameter(xt):
+    # OperationBase(kernel_name, npubin_path = "") as operation_base.h:130-133
+    assert xt.operation_base_paths("k", "/x/k.npubin") == ("k", "/x/k.npubin")
+    assert xt.operation_base_paths("k", None) == ("k", "")

@@ -16,14 +16,19 @@ namespace xllm::kernel::npu {
 
 class OperationBase {
  public:
-  explicit OperationBase(std::string kernel_name) : kernel_name_(std::move(kernel_name)) {}
+  // npubin_path is kept for source compatibility (operation_base.h:130-133);
+  // the kernels are linked in, so it only reports what the caller passed.
+  explicit OperationBase(std::string kernel_name, std::string npubin_path = "")
+      : kernel_name_(std::move(kernel_name)), npubin_path_(std::move(npubin_path)) {}
   virtual ~OperationBase() = default;
   const std::string& kernel_name() const { return kernel_name_; }
+  const std::string& npubin_path() const { return npubin_path_; }
   // Built-in kernels are always available.
   bool is_registered() const { return true; }
 
  private:
   std::string kernel_name_;
+  std::string npubin_path_;
 };
 
 template <auto Fn>

@@ -96,6 +96,10 @@ PYBIND11_MODULE(_xk_torch, m) {
     if (method == "split_rmsnorm_rope") return f.split_rmsnorm_rope().kernel_name();
     return "";
   });
+  m.def("operation_base_paths", [](const std::string& name, std::optional<std::string> path) {
+    npu::OperationBase op = path ? npu::OperationBase(name, *path) : npu::OperationBase(name);
+    return std::make_pair(op.kernel_name(), op.npubin_path());
+  });
   m.def("factory_status_of_invalid_layer_norm", []() {
     // execute() forwards to the C-ABI: an invalid call returns its status.
     return npu::OperationFactory::instance().layer_norm_fwd().execute(

@@ -188,9 +188,11 @@ std::tuple<torch::Tensor, torch::Tensor, torch::Tensor> npu_split_rmsnorm_rope(
   return {q, k, v};
 }
 
-// triton_npu/torch_api/npu_triton_causal_conv1d_update.cpp:22-138
+// triton_npu/torch_api/npu_triton_causal_conv1d_update.cpp:22-138.  As there
+// (`(void)activation`, :38: the kernel is built with SiLU), SiLU is always
+// applied; the C-ABI xk_causal_conv1d_update keeps an activation switch.
 torch::Tensor npu_causal_conv1d_update(
-    torch::Tensor& x, torch::Tensor& conv_state, torch::Tensor& weight, bool activation,
+    torch::Tensor& x, torch::Tensor& conv_state, torch::Tensor& weight, bool /*activation*/,
     const std::optional<torch::Tensor>& bias, const std::optional<torch::Tensor>& cache_seqlens,
     const std::optional<torch::Tensor>& conv_state_indices,
     const std::optional<torch::Tensor>& num_accepted_tokens,
@@ -222,7 +224,8 @@ torch::Tensor npu_causal_conv1d_update(
                                 conv_state.stride(2), w.data_ptr(), w.stride(0), w.stride(1),
                                 ptr(b), xdt(w), static_cast<const int32_t*>(ptr(idx)),
                                 pad_slot_id, conv_state.size(0), out.data_ptr(), out.stride(0),
-                                out.stride(1), out.stride(2), B, D, T, W, S, activation, xdt(xs),
+                                out.stride(1), out.stride(2), B, D, T, W, S, /*activation=*/1,
+                                xdt(xs),
                                 stream_of(x)),
         "xk_causal_conv1d_update");
   return unsq ? out.squeeze(-1) : out;
@@ -313,14 +316,18 @@ torch::Tensor npu_causal_conv1d_update_v2(
   return out;
 }
 
-// triton_npu/torch_api/npu_triton_recurrent_gated_delta_rule.cpp:54-247
+// triton_npu/torch_api/npu_triton_recurrent_gated_delta_rule.cpp:54-247.
+// use_qk_l2norm_in_kernel is accepted and ignored, as there: the reference
+// never passes it to its kernel, which is built with the normalisation on
+// (:216-238; test_fused_recurrent_gated_delta_rule.py:731), so q and k are
+// always l2-normalised.  The C-ABI xk_gdn_recurrent keeps the switch.
 std::pair<torch::Tensor, torch::Tensor> npu_fused_recurrent_gated_delta_rule(
     torch::Tensor& q, torch::Tensor& k, torch::Tensor& v, torch::Tensor& g,
     const std::optional<torch::Tensor>& beta, const std::optional<float>& scale,
     const std::optional<torch::Tensor>& initial_state, bool inplace_final_state,
     const std::optional<torch::Tensor>& cu_seqlens,
     const std::optional<torch::Tensor>& ssm_state_indices,
-    const std::optional<torch::Tensor>& num_accepted_tokens, bool use_qk_l2norm_in_kernel) {
+    const std::optional<torch::Tensor>& num_accepted_tokens, bool /*use_qk_l2norm_in_kernel*/) {
   const int64_t B = k.size(0), T = k.size(1), H = k.size(2), K = k.size(3);
   const int64_t HV = v.size(2), V = v.size(3);
   TORCH_CHECK(has(cu_seqlens) || q.size(0) == 1,
@@ -354,7 +361,7 @@ std::pair<torch::Tensor, torch::Tensor> npu_fused_recurrent_gated_delta_rule(
                          cu.defined() ? xdt(cu) : XK_I32,
                          static_cast<const int32_t*>(ptr(idx)), s0, s1,
                          static_cast<const int32_t*>(ptr(acc)), N, cu.defined() ? 0 : T, H, HV,
-                         K, V, sc, use_qk_l2norm_in_kernel, inplace_final_state, stream_of(q)),
+                         K, V, sc, /*use_qk_l2norm=*/1, inplace_final_state, stream_of(q)),
         "xk_gdn_recurrent");
   return {o, fin};
 }
@@ -413,12 +420,16 @@ std::pair<torch::Tensor, torch::Tensor> npu_fused_gdn_gating(torch::Tensor& A_lo
   return {g, beta_output};
 }
 
-// triton_npu/torch_api/npu_triton_fused_sigmoid_gating_delta_rule_update.cpp:54-177
+// triton_npu/torch_api/npu_triton_fused_sigmoid_gating_delta_rule_update.cpp:54-177.
+// use_qk_l2norm_in_kernel is accepted and ignored, as there: the wrapper
+// never passes it to its kernel (:141-165), whose binary is built by the
+// test that calls it with True (test_fused_sigmoid_gating_delta_rule_update.py:
+// 268-295), so q and k are always l2-normalised.  The C-ABI keeps the switch.
 torch::Tensor npu_fused_sigmoid_gating_delta_rule_update(
     torch::Tensor& A_log, torch::Tensor& a, torch::Tensor& dt_bias, torch::Tensor& q,
     torch::Tensor& k, torch::Tensor& v, torch::Tensor& b, torch::Tensor& initial_state_source,
     torch::Tensor& initial_state_indices, torch::Tensor& cu_seqlens,
-    const std::optional<float>& scale, bool use_qk_l2norm_in_kernel, float softplus_beta,
+    const std::optional<float>& scale, bool /*use_qk_l2norm_in_kernel*/, float softplus_beta,
     float softplus_threshold) {
   for (auto [t, name] : {std::pair<const torch::Tensor*, const char*>{&A_log, "A_log"},
                          {&a, "a"}, {&dt_bias, "dt_bias"}, {&q, "q"}, {&k, "k"}, {&v, "v"},
@@ -472,7 +483,7 @@ torch::Tensor npu_fused_sigmoid_gating_delta_rule_update(
             initial_state_source.size(0),
             static_cast<const int32_t*>(initial_state_indices.data_ptr()),
             static_cast<const int32_t*>(cu_seqlens.data_ptr()), N, H, HV, K, V, sc,
-            use_qk_l2norm_in_kernel, xdt(q), stream_of(q)),
+            /*use_qk_l2norm=*/1, xdt(q), stream_of(q)),
         "xk_gdn_sigmoid_gating_update");
   return o;
 }
@@ -517,6 +528,12 @@ std::pair<torch::Tensor, torch::Tensor> npu_chunk_gated_delta_rule(
   TORCH_CHECK(q.scalar_type() == torch::kBFloat16 && k.scalar_type() == torch::kBFloat16 &&
                   v.scalar_type() == torch::kBFloat16,
               "chunk_gated_delta_rule expects q/k/v to be bfloat16.");
+  if (has(initial_state)) {  // reference :574-579
+    const auto st = initial_state->scalar_type();
+    TORCH_CHECK(st == torch::kBFloat16 || st == torch::kFloat32,
+                "chunk_gated_delta_rule expects initial_state to be bfloat16 or float32, got ",
+                st);
+  }
   const int64_t B = q.size(0), T = q.size(1), H = q.size(2), K = q.size(3);
   const int64_t HV = v.size(2), V = v.size(3);
   TORCH_CHECK(q.sizes() == k.sizes(), "q and k must have the same shape.");
@@ -694,6 +711,26 @@ torch::Tensor npu_gdn_conv_decode(
   const int64_t B = mixed_qkv.size(0), D = mixed_qkv.size(1);
   TORCH_CHECK(D == 2 * num_heads_qk * head_k + num_heads_v * head_v,
               "mixed_qkv width does not match the head layout");
+  // The kernels index ssm_state as dense fp32 [slots, HV, K, V] (slot stride
+  // from stride(0)) and conv_state in mixed_qkv's dtype.
+  TORCH_CHECK(ssm_state.scalar_type() == torch::kFloat32, "ssm_state must be float32");
+  TORCH_CHECK(ssm_state.dim() == 4 && ssm_state.size(1) == num_heads_v &&
+                  ssm_state.size(2) == head_k && ssm_state.size(3) == head_v,
+              "ssm_state must have shape [slots, num_heads_v, head_k, head_v]");
+  TORCH_CHECK(ssm_state.stride(3) == 1 && ssm_state.stride(2) == head_v &&
+                  ssm_state.stride(1) == head_k * head_v,
+              "ssm_state must be contiguous within each slot");
+  TORCH_CHECK(conv_state.scalar_type() == mixed_qkv.scalar_type(),
+              "conv_state must have mixed_qkv's dtype");
+  TORCH_CHECK(conv_state.dim() == 3 && conv_state.size(1) == D,
+              "conv_state must have shape [lines, D, state_len]");
+  TORCH_CHECK(conv_weight.dim() == 2 && conv_weight.size(0) == D,
+              "conv_weight must have shape [D, width]");
+  TORCH_CHECK(g.dim() == 2 && g.size(0) == B && g.size(1) == num_heads_v,
+              "g must have shape [B, num_heads_v]");
+  TORCH_CHECK(!has(beta) || (beta->dim() == 2 && beta->size(0) == B &&
+                             beta->size(1) == num_heads_v),
+              "beta must have shape [B, num_heads_v]");
   const float sc = scale.has_value() ? *scale : 1.0f / std::sqrt(static_cast<float>(head_k));
   auto x = mixed_qkv.stride(1) == 1 ? mixed_qkv : mixed_qkv.contiguous();
   torch::Tensor cb, ci, si, bc;

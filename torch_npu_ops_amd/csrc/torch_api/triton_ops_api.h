@@ -7,8 +7,10 @@
 //
 // Differences from the reference, all deliberate:
 //  * a failed launch throws (c10::Error) instead of being logged;
-//  * conv1d's `activation` and the recurrent op's `use_qk_l2norm_in_kernel`
-//    are honoured (the reference binaries bake SiLU / l2norm in);
+//  * none on the flags the reference binaries bake in: as there,
+//    npu_causal_conv1d_update always applies SiLU (`activation` is ignored)
+//    and the recurrent and sigmoid-gating GDN ops always l2-normalise q and
+//    k (`use_qk_l2norm_in_kernel` is ignored); the C-ABI keeps both switches;
 //  * fp32 inputs are accepted where the reference binaries were bf16-only
 //    (split_rmsnorm_rope, l2norm);
 //  * the chunked op runs its whole pipeline on the device without reading

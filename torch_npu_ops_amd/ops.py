@@ -811,9 +811,30 @@ def gdn_conv_decode(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
     """One fused decode step: conv1d update + SiLU of mixed_qkv [B, D],
     split into q / k / v heads, l2norm, one gated-delta-rule step on
     ssm_state (updated in place).  Returns o [B, HV, V]."""
+    if mixed_qkv.dim() != 2:
+        raise ValueError("gdn_conv_decode expects mixed_qkv [B, D]")
     B, D = mixed_qkv.shape
     if D != 2 * num_heads_qk * head_k + num_heads_v * head_v:
         raise ValueError("mixed_qkv width does not match the head layout")
+    # The kernel indexes ssm_state as dense fp32 [slots, HV, K, V] (slot
+    # stride from stride(0)) and conv_state in mixed_qkv's dtype.
+    if ssm_state.dtype != torch.float32:
+        raise ValueError("ssm_state must be float32")
+    if (ssm_state.dim() != 4
+            or tuple(ssm_state.shape[1:]) != (num_heads_v, head_k, head_v)):
+        raise ValueError("ssm_state must have shape [slots, num_heads_v, head_k, head_v]")
+    if ssm_state.stride()[1:] != (head_k * head_v, head_v, 1):
+        raise ValueError("ssm_state must be contiguous within each slot")
+    if conv_state.dtype != mixed_qkv.dtype:
+        raise ValueError("conv_state must have mixed_qkv's dtype")
+    if conv_state.dim() != 3 or conv_state.size(1) != D:
+        raise ValueError("conv_state must have shape [lines, D, state_len]")
+    if conv_weight.dim() != 2 or conv_weight.size(0) != D:
+        raise ValueError("conv_weight must have shape [D, width]")
+    if tuple(g.shape) != (B, num_heads_v):
+        raise ValueError("g must have shape [B, num_heads_v]")
+    if beta is not None and tuple(beta.shape) != (B, num_heads_v):
+        raise ValueError("beta must have shape [B, num_heads_v]")
     sc = float(scale) if scale is not None else 1.0 / math.sqrt(head_k)
     x = mixed_qkv if mixed_qkv.stride(1) == 1 else mixed_qkv.contiguous()
     w = conv_weight
