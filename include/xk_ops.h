@@ -43,6 +43,7 @@ typedef enum xk_dtype {
 #define XK_ERR_INVALID (-1)     /* shape / pointer / value the op rejects */
 #define XK_ERR_UNSUPPORTED (-2) /* dtype or configuration not built */
 #define XK_ERR_WORKSPACE (-3)   /* workspace missing or too small */
+#define XK_ERR_SCRATCH (-4)     /* problem larger than the static scratch */
 
 const char* xk_version(void);
 const char* xk_status_string(int status);
@@ -330,6 +331,26 @@ int xk_gdn_chunk_fwd(
     xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
     int64_t K, int64_t V, float scale, int use_qk_l2norm, void* workspace,
     size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * xk_gdn_chunk_fwd without a workspace argument, for callers that cannot
+ * allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments and results as xk_gdn_chunk_fwd (the same kernels run);
+ * the workspace is a static device buffer of 64 MiB that the library holds
+ * on every GPU it runs on until the process ends.  Calls whose
+ * xk_gdn_chunk_workspace_bytes(total_tokens, N, HV) exceeds 64 MiB return
+ * XK_ERR_SCRATCH (e.g. up to ~6,700 tokens at HV = 32, ~27,000 at HV = 8).
+ * The call allocates nothing; `stream` must belong to the current device.
+ * Every call on one GPU shares that GPU's buffer: calls that overlap in
+ * time on one GPU (other streams, other host threads) race.
+ */
+int xk_gdn_chunk_fwd_noalloc(
+    const void* q, const void* k, const void* v, xk_dtype dtype, const void* g,
+    xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype, void* o,
+    const float* initial_state, float* final_state, const void* cu_seqlens,
+    xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
+    int64_t K, int64_t V, float scale, int use_qk_l2norm, void* stream);
 
 /*
  * The chunked pipeline stage by stage, in the reference's

@@ -49,3 +49,20 @@ def test_empty_input_is_a_no_op_without_gpu():
                                       None, None, 0, 128, 128, 1e-5, 1, 0,
                                       _lib.XK_BF16, _lib.XK_BF16, None)
     assert st == _lib.XK_OK
+
+
+def test_noalloc_chunk_rejects_problems_beyond_its_scratch_without_gpu():
+    # 64 MiB of static scratch: 100k tokens at 32 v-heads need ~2 GB of
+    # records, so the call is refused before any GPU work.
+    lib = _lib.lib()
+    need = lib.xk_gdn_chunk_workspace_bytes(100_000, 8, 32)
+    assert need > 64 << 20
+    st = lib.xk_gdn_chunk_fwd_noalloc(
+        None, None, None, _lib.XK_BF16, None, _lib.XK_F32, None, _lib.XK_BF16, None, None,
+        None, None, _lib.XK_I32, 8, 100_000, 16, 32, 128, 128, 0.1, 1, None)
+    assert st == _lib.XK_ERR_SCRATCH
+    assert "static scratch" in _lib.status_string(st)
+    st = lib.xk_gdn_chunk_fwd_noalloc(
+        None, None, None, _lib.XK_BF16, None, _lib.XK_F32, None, _lib.XK_BF16, None, None,
+        None, None, _lib.XK_I32, -1, 100, 16, 32, 128, 128, 0.1, 1, None)
+    assert st == _lib.XK_ERR_INVALID

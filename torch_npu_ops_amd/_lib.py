@@ -28,7 +28,7 @@ SZ = ctypes.c_size_t
 
 # xk_dtype values (include/xk_ops.h)
 XK_F32, XK_BF16, XK_F16, XK_I32, XK_I64 = 0, 1, 2, 3, 4
-XK_OK, XK_ERR_INVALID, XK_ERR_UNSUPPORTED, XK_ERR_WORKSPACE = 0, -1, -2, -3
+XK_OK, XK_ERR_INVALID, XK_ERR_UNSUPPORTED, XK_ERR_WORKSPACE, XK_ERR_SCRATCH = 0, -1, -2, -3, -4
 
 # Argument lists, in declaration order of include/xk_ops.h.
 SIGNATURES: dict[str, tuple[list, object]] = {
@@ -68,6 +68,9 @@ SIGNATURES: dict[str, tuple[list, object]] = {
     "xk_gdn_chunk_fwd": (
         [P, P, P, INT, P, INT, P, INT, P, P, P, P, INT, I64, I64, I64, I64, I64,
          I64, F32, INT, P, SZ, P], INT),
+    "xk_gdn_chunk_fwd_noalloc": (
+        [P, P, P, INT, P, INT, P, INT, P, P, P, P, INT, I64, I64, I64, I64, I64,
+         I64, F32, INT, P], INT),
     "xk_gdn_stage_workspace_bytes": ([I64], I64),
     "xk_chunk_local_cumsum": ([P, INT, P, I64, I64, P, INT, I64, I64, P], INT),
     "xk_chunk_scaled_dot_kkt": (

@@ -13,6 +13,8 @@ extern "C" const char* xk_status_string(int status) {
       return "unsupported dtype or configuration";
     case XK_ERR_WORKSPACE:
       return "workspace missing or too small";
+    case XK_ERR_SCRATCH:
+      return "problem needs more memory than the static scratch buffer holds";
     default:
       return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status))
                         : "unknown error";

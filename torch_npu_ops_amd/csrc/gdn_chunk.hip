@@ -39,6 +39,9 @@
 //    loaded into registers while chunk c computes, so the chain never waits
 //    on HBM.  Blocks of one (sequence, head) share an XCD (block id mod 8)
 //    and thus its L2 for the shared q/k/record reads.
+#include <atomic>
+#include <mutex>
+
 #include "gdn_common.h"
 
 namespace xk {
@@ -717,4 +720,70 @@ extern "C" int xk_gdn_chunk_fwd(
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (g_dtype == XK_F32) return chunk_beta<128, float>(p, V, beta_dtype, s);
   return chunk_beta<128, bf16>(p, V, beta_dtype, s);
+}
+
+// ---------------------------------------------------------------------------
+// xk_gdn_chunk_fwd_noalloc: the same pipeline with its workspace in a static
+// device buffer.  Each GPU holds its own copy of `scratch` from the moment
+// this code object is loaded on it until the process ends.  In host code the
+// name `scratch` is only a handle for the runtime: the device address of a
+// GPU's copy comes from hipGetSymbolAddress, called once per device with that
+// device current, and only that address is handed to the kernels.  Every call
+// rewrites the parts of the workspace it reads (chunk table, offsets,
+// records) before reading them, so nothing needs clearing between calls.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = int64_t{64} << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of the current device's `scratch` (looked up on the first
+// call per device).  `stream` must belong to the current device.
+int scratch_on_current_device(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return XK_ERR_UNSUPPORTED;
+  hipDevice_t sdev = -1;
+  e = hipStreamGetDevice(stream, &sdev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (sdev != dev) return XK_ERR_INVALID;
+  void* addr = g_scratch_addr[dev].load(std::memory_order_acquire);
+  if (!addr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    addr = g_scratch_addr[dev].load(std::memory_order_relaxed);
+    if (!addr) {
+      e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+      if (e != hipSuccess) return static_cast<int>(e);
+      if (!addr) return XK_ERR_UNSUPPORTED;
+      g_scratch_addr[dev].store(addr, std::memory_order_release);
+    }
+  }
+  *out = addr;
+  return XK_OK;
+}
+
+}  // namespace
+
+extern "C" int xk_gdn_chunk_fwd_noalloc(
+    const void* q, const void* k, const void* v, xk_dtype dtype, const void* g,
+    xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype, void* o,
+    const float* initial_state, float* final_state, const void* cu_seqlens,
+    xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
+    int64_t K, int64_t V, float scale, int use_qk_l2norm, void* stream) {
+  const int64_t need = xk_gdn_chunk_workspace_bytes(total_tokens, N, HV);
+  if (need < 0) return XK_ERR_INVALID;
+  if (need > kNoAllocScratchBytes) return XK_ERR_SCRATCH;
+  if (N == 0 || total_tokens == 0) return XK_OK;
+  void* ws = nullptr;
+  const int st = scratch_on_current_device(static_cast<hipStream_t>(stream), &ws);
+  if (st != XK_OK) return st;
+  return xk_gdn_chunk_fwd(q, k, v, dtype, g, g_dtype, beta, beta_dtype, o, initial_state,
+                          final_state, cu_seqlens, cu_dtype, N, total_tokens, H, HV, K, V,
+                          scale, use_qk_l2norm, ws, static_cast<size_t>(kNoAllocScratchBytes),
+                          stream);
 }
