@@ -37,7 +37,42 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_TFS = 2500.0  # dense bf16
 ROTATE_BYTES = 1 << 30  # >= 1 GiB of distinct buffers per op
 MAX_SETS = 128
-CPU_THREADS = min(16, os.cpu_count() or 1)
+
+
+def _cgroup_cpus():
+    """CPUs granted by the cgroup v2 quota (cpu.max), or None if unlimited."""
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota == "max":
+            return None
+        return max(1, -(-int(quota) // int(period)))
+    except (OSError, ValueError):
+        return None
+
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: every core this process may run on
+    (os.cpu_count(), narrowed by the affinity mask and the cgroup quota when
+    they grant fewer, so the baseline is not run oversubscribed)."""
+    n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        pass
+    q = _cgroup_cpus()
+    return min(n, q) if q else n
 
 REPO = os.path.dirname(os.path.abspath(__file__))
 if REPO not in sys.path:
@@ -68,6 +103,7 @@ class Case:
     kernel = ""
     algo_bytes = 0
     timing = "eager"  # or "graph" for ops shorter than a Python launch
+    source = ""  # the csrc/*.hip file of `kernel`
 
     def sets(self, dev, n):
         raise NotImplementedError
@@ -80,6 +116,7 @@ class LayerNormCase(Case):
     name = "layer_norm_fwd"
     config = ("config 2a: layer_norm_fwd bf16 x[16384,4096], group_size 4096, "
               "affine w~N(1,0.1) b~N(0,0.1), eps 1e-5, outputs y + fp32 mean/rstd")
+    source = "norm.hip"
     kernel = "ln_tile_kernel<TPG=128,NV=4,z=0>"
     M, N = 16384, 4096
     # x + y (bf16) + mean/rstd (fp32) + w/b (bf16)
@@ -122,6 +159,7 @@ class GemmaCase(Case):
     name = "gemma_rms_norm"
     config = ("config 2b: Gemma RMSNorm bf16 x[16384,4096], gamma~N(1,0.1) "
               "applied as (1+gamma), eps 1e-5, outputs y + fp32 rstd")
+    source = "norm.hip"
     kernel = "ln_tile_kernel<TPG=128,NV=4,z=0>"
     M, N = 16384, 4096
     algo_bytes = M * N * 2 * 2 + M * 4 + N * 2
@@ -163,6 +201,7 @@ class GatedRmsNormCase(Case):
               "x and z bf16 [524288, 128] (16384 tokens x 32 heads), group_size 128, "
               "RMS, gate z*sigmoid(z) after the norm, no bias, eps 1e-6; outputs y + "
               "fp32 rstd")
+    source = "norm.hip"
     kernel = "ln_tile_kernel<TPG=8,NV=2,z=1>"
     M, N = 524288, 128
     # x, z, y (bf16) + rstd (fp32) + weight
@@ -205,7 +244,8 @@ class RopeInplaceCase(Case):
     config = ("next row (rope_inplace, GPT-J interleaved partial RoPE): x bf16 "
               "[16384, 16, 512] rotated in place on its last 64 elements, sin / cos "
               "bf16 [16384, 64]")
-    kernel = "rope_inplace_kernel"
+    source = "rope.hip"
+    kernel = "rope_inplace_tok_kernel"
     timing = "graph"
     T, H, HID, RD = 16384, 16, 512, 64
     # rope part of x read + written, sin / cos read (bf16)
@@ -243,6 +283,7 @@ class RopeCase(Case):
     config = ("config 1: split q/k RMSNorm + neox RoPE fp32, 256 tokens, 32 q + "
               "8 kv heads, head_dim 128, eps 1e-6, theta 1e6, sin/cos rows from "
               "positions U[0,4096)")
+    source = "rope.hip"
     kernel = "split_rmsnorm_rope_kernel"
     timing = "graph"
     T, HQ, HKV, HD = 256, 32, 8, 128
@@ -301,6 +342,7 @@ class RopePrefillCase(Case):
     config = ("split q/k RMSNorm + neox RoPE bf16 at prefill size: 16384 tokens, 32 q + "
               "8 kv heads, head_dim 128, eps 1e-6, theta 1e6, cos/sin from int64 "
               "positions U[0,4096) in registers")
+    source = "rope.hip"
     kernel = "split_rmsnorm_rope_tok_kernel"
     T, HQ, HKV, HD = 16384, 32, 8, 128
     # qkv in + q/k/v out (bf16) + positions (int64) + q/k weights + inv_freq
@@ -367,6 +409,7 @@ class ConvPrefillCase(Case):
     config = ("config 3a: causal_conv1d varlen prefill bf16, 8 sequences "
               "(lengths U[512,3584], 16384 tokens), dim 8192, width 4, SiLU, "
               "w~N(0,0.5), zero initial state")
+    source = "conv1d.hip"
     kernel = "conv1d_varlen_kernel"
     T, D, W, NSEQ = 16384, 8192, 4, 8
     # x + y (bf16) + weights + state read/write
@@ -415,6 +458,7 @@ class ConvDecodeCase(Case):
     name = "causal_conv1d_update"
     config = ("config 3b: causal_conv1d decode update bf16, batch 256 x dim 8192, "
               "conv_state [256,8192,3] ~N(0,1), width 4, SiLU, indices arange")
+    source = "conv1d.hip"
     kernel = "conv1d_update_w4_kernel"
     timing = "graph"
     B, D, W = 256, 8192, 4
@@ -476,6 +520,7 @@ class GdnDecodeFusedCase(Case):
     config = ("config 5: recurrent GDN decode fused with causal_conv1d update, "
               "batch 256, 16 qk / 32 v heads, head_dim 128, fp32 state "
               "[256,32,128,128] in place, bf16 mixed_qkv/g/beta")
+    source = "gdn_recurrent.hip"
     kernel = "gdn_conv_decode_kernel"
     I = GdnDecodeInputs
     # state r/w + mixed_qkv + conv_state r/w + conv_w + g/beta + o
@@ -530,6 +575,7 @@ class GdnRecurrentCase(Case):
     config = ("config 5 (unfused a7 form): fused_recurrent_gated_delta_rule, "
               "256 sequences x 1 token, 16 qk / 32 v heads, head_dim 128, "
               "fp32 state in place, in-kernel l2norm")
+    source = "gdn_recurrent.hip"
     kernel = "gdn_recurrent_kernel"
     I = GdnDecodeInputs
     # state r/w + q/k/v + g/beta + o
@@ -582,6 +628,7 @@ class GdnGatingCase(Case):
     config = ("next row (npu_fused_gdn_gating) on the prefill shape: 16384 tokens x 32 "
               "v heads, bf16 a/b ~N(0,1), fp32 A_log ~N(0,1) and dt_bias ~N(0,1); "
               "outputs fp32 g and bf16 beta")
+    source = "gdn_recurrent.hip"
     kernel = "gdn_gating_kernel"
     timing = "graph"
     R, HV = 16384, 32
@@ -626,6 +673,7 @@ class GdnSigmoidGatingCase(Case):
               "decode shapes: 256 sequences x 1 token, 16 qk / 32 v heads, head_dim 128, "
               "fp32 state [256,32,128,128] in place, in-kernel gating from bf16 a/b "
               "and l2norm")
+    source = "gdn_recurrent.hip"
     kernel = "gdn_recurrent_kernel"
     I = GdnDecodeInputs
     # state r/w + q/k/v + a/b + o
@@ -684,6 +732,7 @@ class QkvzbaSplitCase(Case):
     config = ("next row (npu_fused_qkvzba_split_reshape_cat) on the prefill shape: "
               "16384 rows, 16 qk / 32 v heads (2 per qk head), head dims 128, bf16 "
               "mixed_qkvz [16384, 12288] and mixed_ba [16384, 64]")
+    source = "layout.hip"
     kernel = "qkvzba_split_kernel"
     R, NQK, NV, HD = 16384, 16, 32, 128
     W = NQK * (2 * HD + 2 * (NV // NQK) * HD)
@@ -736,6 +785,7 @@ class GdnChunkCase(Case):
               "(lengths U[512,3584], 16384 tokens), 16 qk / 32 v heads, head_dim "
               "128, chunk 64, q/k l2-normalised, g=-softplus(N(0,1)) fp32, "
               "beta=sigmoid(N(0,1)) bf16, h0~N(0,0.02) fp32, outputs o + final state")
+    source = "gdn_chunk.hip"
     kernel = "gdn_chunk_state_kernel"
     T, NSEQ, H, HV, K, V = 16384, 8, 16, 32, 128, 128
     # q/k + v + o (bf16) + g (fp32) + beta (bf16) + h0/ht (fp32)
@@ -802,6 +852,7 @@ class GdnChunkStagedCase(GdnChunkCase):
     config = ("config 4 through the stage-by-stage API (chunk_local_cumsum, "
               "scaled_dot_kkt, solve_tril, recompute_w_u, fwd_h, fwd_o), the "
               "reference's intermediates (A, Ai, w, u, h, v_new) kept in HBM")
+    source = "gdn_stages.hip"
     kernel = "chunk_fwd_h_kernel"
 
     def sets(self, dev, n):
@@ -859,7 +910,8 @@ class L2NormCase(Case):
     name = "l2norm_last_dim"
     config = ("a6a (npu_l2norm_last_dim) on the prefill shape: q or k of config 4 as "
               "rows, bf16 [262144, 128] (16384 tokens x 16 heads), eps 1e-6, bf16 out")
-    kernel = "l2norm_kernel"
+    source = "norm.hip"
+    kernel = "l2norm_team_kernel"
     timing = "graph"
     R, C = 16384 * 16, 128
     algo_bytes = R * C * 2 * 2
@@ -886,6 +938,67 @@ class L2NormCase(Case):
         from oracle import norm as on
         x = self.x
         return (lambda: on.l2norm_last_dim(x, 1e-6), "full shape, fp32 math on bf16 input", 1.0)
+
+
+_MEASURE = None
+
+
+def measure_lib():
+    """libxk_measure.so (bench.py's reference kernels), built next to
+    libxk.so by torch_npu_ops_amd/_build.py."""
+    global _MEASURE
+    if _MEASURE is None:
+        import ctypes
+        path = os.path.join(REPO, "torch_npu_ops_amd", "libxk_measure.so")
+        if not os.path.exists(path):
+            raise RuntimeError(f"{path} is missing: run __graft_entry__.build() first")
+        lib = ctypes.CDLL(path)
+        lib.xkm_empty.argtypes = [ctypes.c_void_p]
+        lib.xkm_empty.restype = ctypes.c_int
+        lib.xkm_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                 ctypes.c_void_p]
+        lib.xkm_copy.restype = ctypes.c_int
+        _MEASURE = lib
+    return _MEASURE
+
+
+class CopyFloorCase(Case):
+    """A plain device copy moving `moved` bytes (half read, half written):
+    the floor of an HBM-bound kernel with the same traffic, timed in the
+    same harness (graph replay, buffers rotated past the Infinity Cache)."""
+    timing = "graph"
+    kernel = "copy16_kernel"
+
+    def __init__(self, moved):
+        self.nbytes = max(16, (moved // 2) // 16 * 16)
+        self.algo_bytes = 2 * self.nbytes
+        self.name = f"copy_{self.algo_bytes}"
+        self.config = f"plain device copy of {self.nbytes} B ({self.algo_bytes} B moved)"
+
+    def sets(self, dev, n):
+        lib = measure_lib()
+        out = []
+        for _ in range(n):
+            src = torch.empty(self.nbytes, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+
+            def run(src=src, dst=dst):
+                _ok(lib.xkm_copy(src.data_ptr(), dst.data_ptr(), self.nbytes, _cur_stream()),
+                    lib)
+            out.append(run)
+        return out
+
+
+class EmptyKernelCase(Case):
+    """The launch floor: an empty kernel, timed like the small ops."""
+    name = "empty_kernel"
+    timing = "graph"
+    kernel = "empty_kernel"
+    algo_bytes = 0
+
+    def sets(self, dev, n):
+        lib = measure_lib()
+        return [lambda: _ok(lib.xkm_empty(_cur_stream()), lib)] * n
 
 
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, RopePrefillCase,
@@ -925,6 +1038,8 @@ def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
     untimed calls."""
     per_set = max(case.algo_bytes, 1)
     nsets = max(2, min(MAX_SETS, -(-ROTATE_BYTES // per_set)))
+    if case.algo_bytes == 0:
+        nsets = 2
     runs = case.sets(dev, nsets)
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream())
@@ -975,7 +1090,7 @@ def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
 
 
 def time_cpu(case: Case):
-    torch.set_num_threads(CPU_THREADS)
+    torch.set_num_threads(cpu_threads())
     run, sample, scale = case.cpu()
     run()  # warm-up
     ts = []
@@ -987,6 +1102,58 @@ def time_cpu(case: Case):
         if time.perf_counter() > budget_end:
             break
     return statistics.median(ts) * scale, sample, len(ts)
+
+
+def source_sha(fname):
+    """Hash of a kernel source file and the headers every kernel includes:
+    recorded with each traffic measurement, so a measurement taken before a
+    kernel changed is not reported as the current kernel's."""
+    import hashlib
+    import glob
+    csrc = os.path.join(REPO, "torch_npu_ops_amd", "csrc")
+    h = hashlib.sha256()
+    for path in [os.path.join(csrc, fname)] + sorted(glob.glob(os.path.join(csrc, "*.h"))):
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+TRAFFIC_JSON = os.path.join(REPO, "profiles", "hbm_traffic_all_configs.json")
+
+
+def measured_traffic(case):
+    """HBM bytes per dispatch of case.kernel from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE runs (scaled by a plain copy) recorded in TRAFFIC_JSON, or
+    None, with a warning, when there is no entry or it was measured on other
+    kernel sources than the current ones."""
+    if not os.path.exists(TRAFFIC_JSON):
+        print(f"[bench] warning: {TRAFFIC_JSON} missing; roofline.traffic is null",
+              file=sys.stderr)
+        return None
+    with open(TRAFFIC_JSON) as f:
+        t = json.load(f)
+    val = t.get("traffic_bytes", {}).get(case.kernel)
+    if val is None:
+        print(f"[bench] warning: no traffic entry for {case.kernel}; roofline.traffic is null",
+              file=sys.stderr)
+        return None
+    rec = t.get("sources", {}).get(case.source)
+    if rec != source_sha(case.source):
+        print(f"[bench] warning: the traffic of {case.kernel} was measured on another "
+              f"version of {case.source}; roofline.traffic is null", file=sys.stderr)
+        return None
+    return round(val)
+
+
+def cpu_host():
+    """What the CPU baseline ran on."""
+    try:
+        aff = len(os.sched_getaffinity(0))
+    except AttributeError:
+        aff = None
+    return {"os_cpu_count": os.cpu_count(), "affinity_cpus": aff,
+            "cgroup_cpus": _cgroup_cpus(), "torch_threads": torch.get_num_threads(),
+            "cpu_model": _cpu_model()}
 
 
 COPY_BYTES = 256 << 20
@@ -1005,6 +1172,23 @@ def copy_calibration(dev, steps):
     print(json.dumps({"copy_calibration_bytes": COPY_BYTES, "dispatches": steps}))
 
 
+def floors(dev, steps, warmup, moved_list):
+    """Launch floor (empty kernel) and same-traffic copy floors, in the
+    graph harness of the small ops."""
+    out = {"empty_kernel_us": round(time_gpu(EmptyKernelCase(), dev, steps, warmup, False)
+                                    * 1e3, 2)}
+    copies = {}
+    for moved in moved_list:
+        c = CopyFloorCase(moved)
+        us = time_gpu(c, dev, steps, warmup, False) * 1e3
+        copies[str(c.algo_bytes)] = {"us": round(us, 2),
+                                     "GB/s": round(c.algo_bytes / (us * 1e-6) / 1e9, 1)}
+        print(f"[bench] floor: copy moving {c.algo_bytes} B: {us:.2f} us", file=sys.stderr,
+              flush=True)
+    out["copies"] = copies
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1016,6 +1200,9 @@ def main():
                     help="time every op with eager launches")
     ap.add_argument("--graph", action="store_true",
                     help="time every op with a HIP graph replay")
+    ap.add_argument("--floors", action="store_true",
+                    help="only time the launch floor (empty kernel) and plain copies moving "
+                         "the bytes of every small (graph-timed) op, and print them as JSON")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run plain 256 MiB device copies (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -1031,6 +1218,12 @@ def main():
     dev = torch.device("cuda:0")
     if args.copy_calibration:
         copy_calibration(dev, args.steps)
+        return
+    if args.floors:
+        small = [c for c in CASES.values() if c.timing == "graph"]
+        fl = floors(dev, args.steps, args.warmup, sorted({c.algo_bytes for c in small}))
+        fl["ops"] = {c.name: c.algo_bytes for c in small}
+        print(json.dumps({"floors": fl}))
         return
     names = [args.op] if args.op else list(CASES)
     headline = args.op or HEADLINE
@@ -1064,6 +1257,13 @@ def main():
             t_mfma = flops / (MFMA_BF16_TFS * 1e12)
             ops[name]["bound"] = "hbm" if t_hbm >= t_mfma else "mfma"
             ops[name]["frac_of_bound"] = round(max(t_hbm, t_mfma) / (ms * 1e-3), 4)
+        if not eager:
+            # The same bytes through a plain copy kernel in the same harness:
+            # how far this small op is from what its traffic allows here.
+            cus = time_gpu(CopyFloorCase(case.algo_bytes), dev, args.steps, args.warmup,
+                           False) * 1e3
+            ops[name]["same_traffic_copy_us"] = round(cus, 2)
+            ops[name]["vs_copy"] = round(ms * 1e3 / cus, 3)
         print(f"[bench] {name}: {ms*1e3:.2f} us/call, {gbs:.0f} GB/s "
               f"({gbs / HBM_PEAK_GBS:.1%} of peak)"
               + (f", {ops[name]['tokens/s']:.3g} tokens/s, "
@@ -1077,8 +1277,9 @@ def main():
         per_tok = getattr(case, "tokens", 0)
         cpu = {"value": round(per_tok / sec) if per_tok else round(case.algo_bytes / sec / 1e9, 2),
                "unit": "tokens/s" if per_tok else "GB/s",
-               "cores": CPU_THREADS, "kind": "port",
-               "sample": f"{sample}; median of {nrun} runs, {sec*1e3:.1f} ms/call"}
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": f"{sample}; median of {nrun} runs, {sec*1e3:.1f} ms/call",
+               **cpu_host()}
         print(f"[bench] cpu baseline {headline}: {sec*1e3:.1f} ms/call",
               file=sys.stderr, flush=True)
         # The chunked prefill's target is stated against its CPU tokens/s.
@@ -1086,20 +1287,13 @@ def main():
             csec, csample, cn = time_cpu(GdnChunkCase())
             ops[GdnChunkCase.name]["cpu_baseline"] = {
                 "value": round(GdnChunkCase.tokens / csec), "unit": "tokens/s",
-                "cores": CPU_THREADS, "kind": "port",
+                "cores": torch.get_num_threads(), "kind": "port",
                 "sample": f"{csample}; median of {cn} runs, scaled to the full "
-                          f"config: {csec*1e3:.0f} ms/call"}
+                          f"config: {csec*1e3:.0f} ms/call",
+                **cpu_host()}
             print(f"[bench] cpu baseline {GdnChunkCase.name}: {csec*1e3:.0f} ms/call",
                   file=sys.stderr, flush=True)
-    # HBM bytes per dispatch of the headline kernel, as measured by the
-    # rocprofv3 FETCH_SIZE / WRITE_SIZE runs (scaled by a plain copy) that
-    # profiles/hbm_traffic_all_configs.md records; null if absent.
-    traffic = None
-    tpath = os.path.join(REPO, "profiles", "hbm_traffic_all_configs.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            t = json.load(f).get("traffic_bytes", {}).get(case.kernel)
-        traffic = round(t) if t is not None else None
+    traffic = measured_traffic(case)
     line = {
         "metric": "achieved HBM GB/s (% of peak) per op; chunked GDN prefill tokens/s",
         "value": head["GB/s"],

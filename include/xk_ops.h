@@ -174,7 +174,9 @@ int xk_causal_conv1d_update(
  *     (state_len_run = eff - (max_query_len - len)); 1 keeps the last
  *     eff = width-1 (+ max_query_len-1 with spec decoding) inputs of every
  *     sequence.  Sequences whose input slot is pad_slot_id are skipped.
- *   width in [1, 8]; launches two kernels (conv, then final states).
+ *   width in [1, 8]; one kernel (the lane that reads a sequence's history
+ *   writes its final state).  A sequence's input slot must not be another
+ *   sequence's output slot in the same call.
  */
 int xk_causal_conv1d_varlen(
     const void* x, int64_t stride_x_token, int64_t num_tokens, void* out,

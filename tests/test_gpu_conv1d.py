@@ -250,3 +250,28 @@ def test_v2_spec_decoding(dev):
                                           num_accepted_tokens=acc.to(dev))
     torch.testing.assert_close(out.float().cpu(), ref, **BF16_TOL)
     assert torch.equal(st_d.cpu(), ref_state.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("W", [3, 4, 5, 6])
+def test_v2_history_read_next_to_a_tile_edge(dev, W):
+    # Sequences starting 1..W-2 tokens before a 16-token tile edge: their
+    # first W-1 tokens (whose windows read the conv-state history) straddle
+    # the edge.  The final state is written in place into the input slot
+    # (in = out), so the history must be read before it is overwritten.
+    from torch_npu_ops_amd import ops
+    g = torch.Generator().manual_seed(40 + W)
+    qsl = torch.tensor([0, 14, 31, 47, 49, 62, 95, 96, 127, 160], dtype=torch.int32)
+    D = 256
+    B = qsl.numel() - 1
+    x = _rn((160, D), g, torch.bfloat16)
+    state = _rn((B + 1, D, W - 1), g, torch.bfloat16)
+    w = _rn((D, W), g, torch.bfloat16, 0.5)
+    slots = torch.randperm(B + 1, generator=g)[:B].to(torch.int32)
+    for rule in (0, 1):
+        ref, ref_state = oc.causal_conv1d_update_v2(x, state, w, None, True, slots, qsl, 33,
+                                                    state_rule=rule)
+        st_d = state.to(dev)
+        out = ops.npu_causal_conv1d_update_v2(x.to(dev), st_d, w.to(dev), True, None,
+                                              slots.to(dev), qsl.to(dev), 33, state_rule=rule)
+        torch.testing.assert_close(out.float().cpu(), ref, **BF16_TOL)
+        assert torch.equal(st_d.cpu(), ref_state.to(torch.bfloat16))

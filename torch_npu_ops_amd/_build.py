@@ -84,6 +84,28 @@ def build_lib(jobs: int | None = None, verbose: bool = True) -> str:
     return LIB_PATH
 
 
+MEASURE_DIR = os.path.join(PKG_DIR, "measure")
+MEASURE_LIB_PATH = os.path.join(PKG_DIR, "libxk_measure.so")
+
+
+def build_measure_lib(verbose: bool = True) -> str:
+    """libxk_measure.so: bench.py's reference kernels (empty kernel, plain
+    copy).  Measurement only; not part of the C-ABI."""
+    os.makedirs(BUILD_DIR, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(MEASURE_DIR, "*.hip")))
+    objs = []
+    for src in srcs:
+        obj = os.path.join(BUILD_DIR, "measure_" + os.path.basename(src) + ".o")
+        _run([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+        objs.append(obj)
+    tmp = MEASURE_LIB_PATH + ".tmp"
+    _run([HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
+    os.replace(tmp, MEASURE_LIB_PATH)
+    if verbose:
+        print(f"[xk build] linked {MEASURE_LIB_PATH}", flush=True)
+    return MEASURE_LIB_PATH
+
+
 TORCH_API_DIR = os.path.join(CSRC_DIR, "torch_api")
 TORCH_API_PATH = os.path.join(PKG_DIR, "_xk_torch.so")
 
@@ -141,6 +163,7 @@ def build_torch_api(jobs: int | None = None, verbose: bool = True) -> str:
 def build_all(verbose: bool = True) -> None:
     build_lib(verbose=verbose)
     build_torch_api(verbose=verbose)
+    build_measure_lib(verbose=verbose)
 
 
 def clean() -> None:

@@ -250,10 +250,38 @@ __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
   const int64_t cb = bid / p.ntt;
   const int64_t c0 = (cb * 256 + threadIdx.x) * VEC;
   if (c0 >= p.D) return;
+  // Tile k covers tokens [tile_edge(k * kTileT), tile_edge((k + 1) * kTileT)):
+  // an edge that falls inside the first W-1 tokens of a sequence moves to the
+  // end of those tokens.  Every token whose window reaches into the conv
+  // state's history then sits in the tile of its sequence's first token, so
+  // exactly one lane per (sequence, channel group) reads that history -- and
+  // writes the sequence's final state right after reading it (below).  W-1
+  // <= 7 < kTileT, so every tile keeps at least kTileT - 6 tokens.
+  // The sequence holding token t, searched forward from sequence q (with
+  // qsl[q] <= t or q = 0): a few steps cover the usual case (the next
+  // sequence at most), a binary search the rest.  One search per block.
+  auto seq_from = [&](int q, int64_t t) {
+    for (int i = 0; i < 4; ++i) {
+      if (q + 1 >= p.B || p.qsl[q + 1] > t) return q;
+      ++q;
+    }
+    return find_seq(p.qsl, p.B, t);
+  };
+  // Edge b moved out of the first W-1 tokens of its sequence q.
+  auto tile_edge = [&](int q, int64_t b) -> int64_t {
+    if constexpr (W <= 2) {
+      return b;  // the history reaches only the first token of a sequence
+    } else {
+      const int64_t st = p.qsl[q], en = p.qsl[q + 1];
+      return (b > st && b < st + (W - 1) && b < en) ? min(st + (W - 1), en) : b;
+    }
+  };
+  const int64_t e0 = tile * kTileT, e1 = e0 + kTileT;
+  const int s_e0 = find_seq(p.qsl, p.B, e0);
   // Tokens outside [qsl[0], qsl[B]) belong to no sequence and are skipped.
-  const int64_t t0 = max(tile * kTileT, static_cast<int64_t>(p.qsl[0]));
+  const int64_t t0 = max(tile_edge(s_e0, e0), static_cast<int64_t>(p.qsl[0]));
   const int64_t total = p.qsl[p.B];
-  const int64_t t_end = min(min((tile + 1) * kTileT, total), p.num_tokens);
+  const int64_t t_end = min(min(tile_edge(seq_from(s_e0, e1), e1), total), p.num_tokens);
   if (t0 >= t_end) return;
 
   float wt[W][VEC], bs[VEC];
@@ -285,11 +313,52 @@ __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
   for (int u = 0; u < VEC; ++u)
     bs[u] = p.bias ? load_as_f32(p.bias, c0 + u, p.wdt) : 0.f;
 
-  int s = find_seq(p.qsl, p.B, t0);
+  int s = seq_from(s_e0, t0);
   int64_t seq_start = p.qsl[s];
   int64_t seq_end = p.qsl[s + 1];
   float win[W > 1 ? W - 1 : 1][VEC];
   bool skip = false;
+
+  // Final conv state of sequence sq for this lane's channels, written after
+  // the token loop by the lane that read the sequence's history (so an
+  // output slot that is also the input slot is overwritten only after its
+  // history was read).  The state_len_run rule of
+  // triton_causal_conv1d_update_v2_test.cpp:138-223 (state_rule 0), or the
+  // last eff inputs (state_rule 1); with speculative decoding the kept part
+  // starts one column after the accepted token's window
+  // (test_causal_conv1d_update_v2.py:326-333).
+  auto write_state = [&](int sq) {
+    const int64_t start = p.qsl[sq], len = p.qsl[sq + 1] - start;
+    if (len <= 0 || start < 0 || start + len > p.num_tokens) return;
+    const int64_t in_slot = resolve_slot(p, sq, p.init_idx);
+    if (p.slots && in_slot == p.pad) return;
+    const int s = sq;
+    const int64_t out_slot = resolve_slot(p, s, p.last_idx);
+    if (out_slot < 0 || out_slot >= p.lines) return;
+    const bool in_valid = in_slot >= 0 && in_slot < p.lines;
+    const int64_t run = p.state_rule == 0
+                            ? p.eff_state_len - (p.max_query_len - len)
+                            : p.eff_state_len;
+    if (run <= 0 || run > p.S) return;
+    const int64_t off = p.accepted ? p.accepted[s] - 1 : 0;
+    const int64_t shift = p.accepted ? 1 : len;
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) {
+      const int64_t c = c0 + u;
+      T* dst = reinterpret_cast<T*>(p.state) + out_slot * p.ssl + c * p.ssd;
+      const T* src = reinterpret_cast<const T*>(p.state) + in_slot * p.ssl + c * p.ssd;
+      const T* xs = reinterpret_cast<const T*>(p.x) + start * p.sx + c;
+      if (len >= run) {
+        for (int64_t i = 0; i < run; ++i) dst[i * p.sss] = xs[(len - run + i) * p.sx];
+      } else {
+        const int64_t keep = run - len;
+        if (in_valid && off >= 0)
+          for (int64_t i = 0; i < keep && off + shift + i < p.S; ++i)
+            dst[i * p.sss] = src[(off + shift + i) * p.sss];  // reads run ahead of writes
+        for (int64_t i = 0; i < len; ++i) dst[(keep + i) * p.sss] = xs[i * p.sx];
+      }
+    }
+  };
 
   // Loads the state history of sequence s and, for a tile starting inside
   // the sequence, the preceding inputs, into the window.
@@ -317,6 +386,7 @@ __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
       }
     }
   };
+  const int s_first = s;
   enter(t0);
 
   // One token through the window: returns the output vector.
@@ -394,42 +464,10 @@ __global__ void __launch_bounds__(256) conv1d_varlen_kernel(VarlenParams p) {
     xp += p.sx;
     op += p.so;
   }
-}
-
-// Final conv state of each sequence (after the conv kernel has read every
-// history).  One lane per (sequence, channel).
-template <typename T>
-__global__ void __launch_bounds__(256) conv1d_varlen_state_kernel(VarlenParams p) {
-  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (gid >= static_cast<int64_t>(p.B) * p.D) return;
-  const int s = static_cast<int>(gid / p.D);
-  const int64_t c = gid - static_cast<int64_t>(s) * p.D;
-  const int64_t start = p.qsl[s];
-  const int64_t len = p.qsl[s + 1] - start;
-  if (len <= 0 || start < 0 || start + len > p.num_tokens) return;
-  const int64_t in_slot = resolve_slot(p, s, p.init_idx);
-  if (p.slots && in_slot == p.pad) return;
-  const int64_t out_slot = resolve_slot(p, s, p.last_idx);
-  if (out_slot < 0 || out_slot >= p.lines) return;
-  const bool in_valid = in_slot >= 0 && in_slot < p.lines;
-  const int64_t run = p.state_rule == 0
-                          ? p.eff_state_len - (p.max_query_len - len)
-                          : p.eff_state_len;
-  if (run <= 0 || run > p.S) return;
-  const int64_t off = p.accepted ? p.accepted[s] - 1 : 0;
-  const int64_t shift = p.accepted ? 1 : len;
-  T* dst = reinterpret_cast<T*>(p.state) + out_slot * p.ssl + c * p.ssd;
-  const T* src = reinterpret_cast<const T*>(p.state) + in_slot * p.ssl + c * p.ssd;
-  const T* x = reinterpret_cast<const T*>(p.x) + start * p.sx + c;
-  if (len >= run) {
-    for (int64_t i = 0; i < run; ++i) dst[i * p.sss] = x[(len - run + i) * p.sx];
-  } else {
-    const int64_t keep = run - len;
-    if (in_valid && off >= 0)
-      for (int64_t i = 0; i < keep && off + shift + i < p.S; ++i)
-        dst[i * p.sss] = src[(off + shift + i) * p.sss];  // reads run ahead
-    for (int64_t i = 0; i < len; ++i) dst[(keep + i) * p.sss] = x[i * p.sx];
-  }
+  // Final states of the sequences whose first token lies in this tile:
+  // their histories were all read above, by this lane.
+  for (int sq = s_first; sq < p.B && p.qsl[sq] < t_end; ++sq)
+    if (p.qsl[sq] >= t0) write_state(sq);
 }
 
 template <typename T, int VEC>
@@ -451,10 +489,6 @@ int launch_varlen_w(VarlenParams p, hipStream_t s) {
 #undef XK_W
     default: return XK_ERR_UNSUPPORTED;
   }
-  int st = launch_status();
-  if (st) return st;
-  hipLaunchKernelGGL((conv1d_varlen_state_kernel<T>),
-                     dim3(cdiv(static_cast<int64_t>(p.B) * p.D, 256)), dim3(256), 0, s, p);
   return launch_status();
 }
 

@@ -1,0 +1,41 @@
+// Reference kernels for bench.py's floors: an empty kernel (the launch
+// floor) and a plain device copy (the floor of an HBM-bound kernel that
+// moves the same bytes).  Measurement only: built into libxk_measure.so,
+// loaded by bench.py, and not part of the C-ABI in include/xk_ops.h.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ void empty_kernel() {}
+
+// One 16-byte vector per lane, non-temporal in and out: the access pattern
+// of the row kernels it is compared with.
+__global__ void __launch_bounds__(256) copy16_kernel(const u32x4* __restrict__ src,
+                                                     u32x4* __restrict__ dst, int64_t n16) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+}  // namespace
+
+extern "C" int xkm_empty(void* stream) {
+  hipLaunchKernelGGL(empty_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream));
+  return static_cast<int>(hipGetLastError());
+}
+
+// Copies `bytes` (a multiple of 16; both pointers 16-byte aligned): reads
+// `bytes` and writes `bytes`.
+extern "C" int xkm_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+  if (bytes <= 0 || bytes % 16 != 0) return -1;
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 != 0) return -1;
+  const int64_t n16 = bytes / 16;
+  const int64_t blocks = (n16 + 255) / 256;
+  if (blocks > INT32_MAX) return -1;
+  hipLaunchKernelGGL(copy16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
+                     static_cast<u32x4*>(dst), n16);
+  return static_cast<int>(hipGetLastError());
+}
