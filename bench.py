@@ -570,6 +570,70 @@ class GdnDecodeFusedCase(Case):
         return run, f"{n} of 256 batch rows (conv update + split + l2norm + GDN step, fp32)", a.B / n
 
 
+class GdnDecodeGatedCase(Case):
+    name = "gdn_decode_fused_gating"
+    config = ("config 5 from the projection outputs: causal_conv1d update + SiLU + "
+              "split + l2norm + GDN gating (g, beta from a, b, A_log, dt_bias) + one "
+              "GDN step in one launch, batch 256, 16 qk / 32 v heads, head_dim 128, "
+              "fp32 state [256,32,128,128] in place, bf16 mixed_qkv/a/b")
+    source = "gdn_recurrent.hip"
+    kernel = "gdn_conv_decode_kernel"
+    I = GdnDecodeInputs
+    # config 5's bytes with a/b (bf16) in place of g/beta, plus A_log / dt_bias
+    algo_bytes = GdnDecodeFusedCase.algo_bytes + I.HV * 4 * 2
+
+    def __init__(self):
+        self.inp = GdnDecodeInputs()
+        g = torch.Generator().manual_seed(1)
+        I = GdnDecodeInputs
+        self.a = _randn((I.B, I.HV), g, torch.bfloat16)
+        self.b = _randn((I.B, I.HV), g, torch.bfloat16)
+        self.A_log = torch.randn(I.HV, generator=g)
+        self.dt_bias = torch.randn(I.HV, generator=g)
+
+    def sets(self, dev, n):
+        from torch_npu_ops_amd import _lib
+        lib = _lib.lib()
+        a = self.inp
+        cw, idx = a.cw.to(dev), a.idx.to(dev)
+        av, bv = self.a.to(dev), self.b.to(dev)
+        al, db = self.A_log.to(dev), self.dt_bias.to(dev)
+        out = []
+        for _ in range(n):
+            x, cs, st = a.x.to(dev), a.cs.to(dev), a.state.to(dev)
+            o = torch.empty(a.B, a.HV, a.V, dtype=torch.bfloat16, device=dev)
+
+            def run(x=x, cs=cs, st=st, o=o):
+                _ok(lib.xk_gdn_conv_gating_decode(
+                    x.data_ptr(), a.D, cs.data_ptr(), cs.stride(0), cs.stride(1),
+                    cs.stride(2), a.B, a.W - 1, cw.data_ptr(), a.W, 1, None,
+                    _lib.XK_BF16, a.W, idx.data_ptr(), -1, al.data_ptr(), av.data_ptr(),
+                    db.data_ptr(), bv.data_ptr(), _lib.XK_BF16, 1.0, 20.0, st.data_ptr(),
+                    st.stride(0), a.B, idx.data_ptr(), o.data_ptr(), a.B, a.H,
+                    a.HV, a.K, a.V, a.K ** -0.5, 1, _lib.XK_BF16, _cur_stream()), lib)
+            out.append(run)
+        return out
+
+    def cpu(self):
+        from oracle import conv1d as oc
+        from oracle import gating as ogt
+        a = self.inp
+        n = 16  # bounded sample: 16 of the 256 batch rows
+
+        def run():
+            y, _ = oc.causal_conv1d_update(a.x[:n], a.cs[:n], a.cw, None, True,
+                                           a.idx[:n])
+            q = y[:, :a.H * a.K].reshape(1, n, a.H, a.K)
+            k = y[:, a.H * a.K:2 * a.H * a.K].reshape(1, n, a.H, a.K)
+            v = y[:, 2 * a.H * a.K:].reshape(1, n, a.HV, a.V)
+            ogt.sigmoid_gating_delta_rule_update(
+                self.A_log, self.a[:n][None], self.dt_bias, q, k, v, self.b[:n][None],
+                a.state[:n], a.idx[:n], torch.arange(n + 1, dtype=torch.int32),
+                a.K ** -0.5, True, dtype=torch.float32)
+        return (run, f"{n} of 256 batch rows (conv update + split + gating + l2norm + "
+                "GDN step, fp32)", a.B / n)
+
+
 class GdnRecurrentCase(Case):
     name = "gdn_recurrent"
     config = ("config 5 (unfused a7 form): fused_recurrent_gated_delta_rule, "
@@ -1003,7 +1067,8 @@ class EmptyKernelCase(Case):
 
 CASES = {c.name: c for c in (LayerNormCase, GemmaCase, RopeCase, RopePrefillCase,
                              ConvPrefillCase,
-                             ConvDecodeCase, GdnDecodeFusedCase, GdnRecurrentCase,
+                             ConvDecodeCase, GdnDecodeFusedCase, GdnDecodeGatedCase,
+                             GdnRecurrentCase,
                              GdnChunkCase, GdnChunkStagedCase, GdnGatingCase,
                              GdnSigmoidGatingCase, GatedRmsNormCase, QkvzbaSplitCase,
                              RopeInplaceCase, L2NormCase)}

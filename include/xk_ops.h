@@ -307,6 +307,30 @@ int xk_gdn_conv_decode(
     int use_qk_l2norm, xk_dtype dtype, void* stream);
 
 /* ------------------------------------------------------------------------
+ * xk_gdn_conv_decode with the GDN gating computed in the kernel (the decode
+ * step from the projection outputs in one launch): per (row, v head) the
+ * log-decay g = -exp(A_log) * softplus_{softplus_beta, threshold}(a +
+ * dt_bias) and beta = sigmoid(b), in fp32 registers, as
+ * xk_gdn_sigmoid_gating_update forms them (reference pair:
+ * npu_triton_fused_sigmoid_gating_delta_rule_update.cpp:54-177 after
+ * npu_causal_conv1d_update).  a, b : [B, HV] in ab_dtype; A_log, dt_bias :
+ * fp32 [HV].  Every other argument as xk_gdn_conv_decode; a state index
+ * outside [0, num_slots) starts from a zero state and writes nothing.
+ */
+int xk_gdn_conv_gating_decode(
+    const void* mixed_qkv, int64_t stride_x_row, void* conv_state,
+    int64_t stride_cs_line, int64_t stride_cs_dim, int64_t stride_cs_tok,
+    int64_t conv_lines, int64_t conv_state_len, const void* conv_weight,
+    int64_t stride_w_dim, int64_t stride_w_tap, const void* conv_bias,
+    xk_dtype w_dtype, int64_t width, const int32_t* conv_state_indices,
+    int32_t pad_slot_id, const float* A_log, const void* a, const float* dt_bias,
+    const void* b, xk_dtype ab_dtype, float softplus_beta, float threshold,
+    float* ssm_state, int64_t stride_state_slot, int64_t num_slots,
+    const int32_t* ssm_state_indices, void* o, int64_t B, int64_t H, int64_t HV,
+    int64_t K, int64_t V, float scale, int use_qk_l2norm, xk_dtype dtype,
+    void* stream);
+
+/* ------------------------------------------------------------------------
  * Chunked gated delta rule (prefill), chunk size 64.
  * Replaces xllm::kernel::npu::npu_chunk_gated_delta_rule
  *   (triton_npu/torch_api/triton_ops_api.h:111-122,

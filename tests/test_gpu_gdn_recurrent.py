@@ -177,3 +177,64 @@ def test_fused_conv_decode(dev, B, H, HV, pads):
     torch.testing.assert_close(o[live].float().cpu(), ref_o.float(), **O_TOL)
     assert torch.equal(cs_d.cpu(), ref_cs.to(torch.bfloat16))
     assert_state_close(st_d.cpu(), ref_st.float())
+
+
+def test_fused_conv_decode_scalar_conv_path(dev):
+    # fp32 conv weights and a conv state longer than the window take the
+    # per-channel conv path of the fused kernel (not the 8-channel vectors).
+    from torch_npu_ops_amd import ops
+    B, H, HV = 6, 2, 4
+    x, cs, w, g, beta, st, cidx = _fused_case(B, H, HV, 77, (1,))
+    live, ref_o, ref_cs, ref_st = _fused_ref(x, cs, w.float(), g, beta, st, cidx, H, HV)
+    cs_d, st_d = cs.to(dev), st.to(dev)
+    o = ops.gdn_conv_decode(x.to(dev), cs_d, w.float().to(dev), g.to(dev), beta.to(dev),
+                            st_d, H, HV, conv_state_indices=cidx.to(dev),
+                            ssm_state_indices=cidx.clamp(min=0).to(dev))
+    torch.testing.assert_close(o[live].float().cpu(), ref_o.float(), **O_TOL)
+    assert torch.equal(cs_d.cpu(), ref_cs.to(torch.bfloat16))
+    assert_state_close(st_d.cpu(), ref_st.float())
+
+
+def _gated_ref(x, cs, w, A_log, a, dt_bias, b, st, cidx, sidx, H, HV):
+    """conv1d update + SiLU (oracle/conv1d.py), the [q | k | v] split, then
+    the sigmoid-gating recurrent update (oracle/gating.py, kernel arithmetic,
+    float64) on the live rows."""
+    from oracle import gating as ogt
+    B = x.shape[0]
+    y, cs_new = oc.causal_conv1d_update(x, cs, w, None, True, cidx, -1)
+    live = [r for r in range(B) if int(cidx[r]) != -1]
+    q = y[live, :H * 128].reshape(1, len(live), H, 128)
+    k = y[live, H * 128:2 * H * 128].reshape(1, len(live), H, 128)
+    v = y[live, 2 * H * 128:].reshape(1, len(live), HV, 128)
+    o, st_new = ogt.sigmoid_gating_delta_rule_update(
+        A_log, a[live][None], dt_bias, q, k, v, b[live][None], st, sidx[live],
+        torch.arange(len(live) + 1, dtype=torch.int32), 128 ** -0.5, True)
+    return live, o[0], cs_new, st_new
+
+
+@pytest.mark.parametrize("B,H,HV,pads,neg", [(256, 16, 32, (), ()), (5, 4, 4, (2,), (4,)),
+                                              (3, 2, 8, (), (1,)), (4, 8, 24, (0, 3), ())])
+def test_fused_conv_gating_decode(dev, B, H, HV, pads, neg):
+    # (256, 16, 32) is BASELINE config 5 with the gating in the kernel: the
+    # decode step from the projection outputs (mixed_qkv, a, b) in one launch.
+    # `neg` rows have a negative state index: zero initial state, no write.
+    from torch_npu_ops_amd import ops
+    x, cs, w, _, _, st, cidx = _fused_case(B, H, HV, 3 * B + H, pads)
+    gen = torch.Generator().manual_seed(B)
+    a = torch.randn(B, HV, generator=gen).to(torch.bfloat16)
+    b = torch.randn(B, HV, generator=gen).to(torch.bfloat16)
+    A_log = torch.randn(HV, generator=gen)
+    dt_bias = torch.randn(HV, generator=gen)
+    sidx = cidx.clamp(min=0)
+    for r in neg:
+        sidx[r] = -1
+    live, ref_o, ref_cs, ref_st = _gated_ref(x, cs, w, A_log, a, dt_bias, b, st, cidx, sidx,
+                                             H, HV)
+    cs_d, st_d = cs.to(dev), st.to(dev)
+    o = ops.gdn_conv_gating_decode(x.to(dev), cs_d, w.to(dev), A_log.to(dev), a.to(dev),
+                                   dt_bias.to(dev), b.to(dev), st_d, H, HV,
+                                   conv_state_indices=cidx.to(dev),
+                                   ssm_state_indices=sidx.to(dev))
+    torch.testing.assert_close(o[live].float().cpu(), ref_o.float(), **O_TOL)
+    assert torch.equal(cs_d.cpu(), ref_cs.to(torch.bfloat16))
+    assert_state_close(st_d.cpu(), ref_st.float())

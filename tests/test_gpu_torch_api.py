@@ -255,3 +255,22 @@ def test_sigmoid_gating_update_always_normalises_like_the_reference(dev, xt):
     torch.testing.assert_close(o.float().cpu().reshape(ro.shape), ro.float(), rtol=1.6e-2,
                                atol=1e-2)
     assert_state_close(st.cpu(), rs.float())
+
+
+def test_gdn_conv_gating_decode_paths(dev, xt):
+    from torch_npu_ops_amd import ops
+    g = _g(12)
+    B, H, HV, D = 4, 2, 4, 128
+    W = 2 * H * D + HV * D
+    x = torch.randn(B, W, generator=g).bfloat16().to(dev)
+    cs = torch.randn(B, W, 3, generator=g).bfloat16().to(dev)
+    cw = (torch.randn(W, 4, generator=g) * 0.5).bfloat16().to(dev)
+    a = torch.randn(B, HV, generator=g).bfloat16().to(dev)
+    b = torch.randn(B, HV, generator=g).bfloat16().to(dev)
+    A_log = torch.randn(HV, generator=g).to(dev)
+    dt_bias = torch.randn(HV, generator=g).to(dev)
+    st = (torch.randn(B, HV, D, D, generator=g) * 0.02).to(dev)
+    c1, c2, s1, s2 = cs.clone(), cs.clone(), st.clone(), st.clone()
+    o1 = ops.gdn_conv_gating_decode(x, c1, cw, A_log, a, dt_bias, b, s1, H, HV)
+    o2 = xt.npu_gdn_conv_sigmoid_gating_decode(x, c2, cw, A_log, a, dt_bias, b, s2, H, HV)
+    assert torch.equal(o1, o2) and torch.equal(c1, c2) and torch.equal(s1, s2)

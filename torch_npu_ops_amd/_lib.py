@@ -64,6 +64,10 @@ SIGNATURES: dict[str, tuple[list, object]] = {
         [P, I64, P, I64, I64, I64, I64, I64, P, I64, I64, P, INT, I64, P, I32,
          P, INT, P, INT, P, I64, I64, P, P, I64, I64, I64, I64, I64, F32, INT,
          INT, P], INT),
+    "xk_gdn_conv_gating_decode": (
+        [P, I64, P, I64, I64, I64, I64, I64, P, I64, I64, P, INT, I64, P, I32,
+         P, P, P, P, INT, F32, F32, P, I64, I64, P, P, I64, I64, I64, I64, I64,
+         F32, INT, INT, P], INT),
     "xk_gdn_chunk_workspace_bytes": ([I64, I64, I64], I64),
     "xk_gdn_chunk_fwd": (
         [P, P, P, INT, P, INT, P, INT, P, P, P, P, INT, I64, I64, I64, I64, I64,

@@ -431,7 +431,60 @@ struct FusedParams {
   float scale;
   int l2norm;
   int32_t pad;
+  // Conv state [lines, D, S] with S contiguous per channel and lines 16-byte
+  // aligned, weights [D, W] contiguous in x's dtype, W - 1 == S <= 8: eight
+  // channels per lane with 16-byte loads and stores.
+  int conv_vec;
+  // Gating mode: g holds a and beta holds b ([B, HV]); g = gdn_log_decay(a +
+  // dt_bias, A_log) and beta = sigmoid(b), per head, in registers.
+  int gating;
+  const float* A_log;
+  const float* dt_bias;
+  float sp_beta, sp_thr;
 };
+
+// Conv update + SiLU of 8 consecutive channels c0..c0+7 of batch row b
+// (FusedParams::conv_vec layout); writes the shifted state back.
+template <typename T, int S>
+__device__ __forceinline__ void conv8(const FusedParams& p, int64_t b, int64_t cslot,
+                                      bool conv_ok, int64_t c0, float (&y)[8]) {
+  using V8 = Vec<T, 8>;
+  constexpr int W = S + 1;
+  const V8 xv = ld_stream(reinterpret_cast<const V8*>(reinterpret_cast<const T*>(p.x) +
+                                                      b * p.sx + c0));
+  Arr<T, 8 * W> wv;  // weights of the 8 channels, channel-major
+#pragma unroll
+  for (int q = 0; q < W; ++q)
+    *reinterpret_cast<V8*>(&wv.v[8 * q]) =
+        reinterpret_cast<const V8*>(reinterpret_cast<const T*>(p.w) + c0 * W)[q];
+  Arr<T, 8 * S> sv;  // state of the 8 channels, channel-major
+  T* st = reinterpret_cast<T*>(p.conv_state) + cslot * p.cs_line + c0 * S;
+  if (conv_ok) {
+#pragma unroll
+    for (int q = 0; q < S; ++q)
+      *reinterpret_cast<V8*>(&sv.v[8 * q]) = ld_stream(reinterpret_cast<const V8*>(st) + q);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8 * S; ++e) sv.v[e] = from_f32<T>(0.f);
+  }
+  Arr<T, 8 * S> ns;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    float acc = p.cbias ? load_as_f32(p.cbias, c0 + c, p.wdt) : 0.f;
+#pragma unroll
+    for (int j = 0; j < S; ++j) acc = fmaf(to_f32(sv.v[c * S + j]), to_f32(wv.v[c * W + j]), acc);
+    acc = fmaf(to_f32(xv.v[c]), to_f32(wv.v[c * W + S]), acc);
+    y[c] = silu(acc);
+#pragma unroll
+    for (int j = 0; j + 1 < S; ++j) ns.v[c * S + j] = sv.v[c * S + j + 1];
+    ns.v[c * S + S - 1] = xv.v[c];
+  }
+  if (conv_ok) {
+#pragma unroll
+    for (int q = 0; q < S; ++q)
+      st_stream(reinterpret_cast<V8*>(st) + q, *reinterpret_cast<const V8*>(&ns.v[8 * q]));
+  }
+}
 
 template <int K, int V, typename T, typename GT, typename BT>
 __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p) {
@@ -449,6 +502,39 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
   // Conv update for the group's channels: q (K), k (K), then R * V of v.
   const int nch = 2 * K + R * V;
   const bool conv_ok = cslot >= 0 && cslot < p.conv_lines;
+  const bool st_ok = sslot >= 0 && sslot < p.slots;
+  // The first v head's state tile is requested before the conv phase, so
+  // its 64 KB stream overlaps the conv loads and arithmetic.
+  Tile<K, V> t;
+  {
+    float* sbase = p.state + sslot * p.st_slot_stride + static_cast<int64_t>(h) * R * K * V;
+    if (st_ok) load_tile<K, V>(t, sbase); else zero_tile<K, V>(t);
+  }
+  // Global channel of group channel i: q (K), k (K), then R * V of v.
+  auto chan = [&](int i) -> int64_t {
+    if (i < K) return static_cast<int64_t>(h) * K + i;
+    if (i < 2 * K) return static_cast<int64_t>(p.H) * K + static_cast<int64_t>(h) * K + (i - K);
+    return 2 * static_cast<int64_t>(p.H) * K + static_cast<int64_t>(h) * R * V + (i - 2 * K);
+  };
+  auto put = [&](int i, float y) {
+    if (i < 2 * K) xv_lds[i] = y;
+    else vv_lds[(i - 2 * K) / V][(i - 2 * K) % V] = y;
+  };
+  if (p.conv_vec) {
+    // 8 channels per lane (K and V are multiples of 8, so a group never
+    // straddles the q / k / v parts).
+    for (int i = tid * 8; i < nch; i += kThreads * 8) {
+      float y[8];
+      switch (p.S) {
+        case 1: conv8<T, 1>(p, b, cslot, conv_ok, chan(i), y); break;
+        case 2: conv8<T, 2>(p, b, cslot, conv_ok, chan(i), y); break;
+        case 3: conv8<T, 3>(p, b, cslot, conv_ok, chan(i), y); break;
+        default: conv8<T, 4>(p, b, cslot, conv_ok, chan(i), y); break;
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) put(i + c, y[c]);
+    }
+  } else {
   for (int i = tid; i < nch; i += kThreads) {
     int64_t ch;
     if (i < K) ch = static_cast<int64_t>(h) * K + i;
@@ -468,22 +554,27 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
       for (int j = 0; j + 1 < p.S; ++j) st[j * p.cs_tok] = st[(j + 1) * p.cs_tok];
       st[(p.S - 1) * p.cs_tok] = reinterpret_cast<const T*>(p.x)[b * p.sx + ch];
     }
-    if (i < 2 * K) xv_lds[i] = y;
-    else vv_lds[(i - 2 * K) / V][(i - 2 * K) % V] = y;
+    put(i, y);
+  }
   }
   __syncthreads();
 
-  const bool st_ok = sslot >= 0 && sslot < p.slots;
   for (int j = 0; j < R; ++j) {
     const int hv = h * R + j;
-    Tile<K, V> t;
     float* sbase = p.state + sslot * p.st_slot_stride + static_cast<int64_t>(hv) * K * V;
-    if (st_ok) load_tile<K, V>(t, sbase); else zero_tile<K, V>(t);
+    if (j > 0) {
+      if (st_ok) load_tile<K, V>(t, sbase); else zero_tile<K, V>(t);
+    }
     prep_qk<K, V>(sm, [&](int which, int e) { return xv_lds[which * K + e]; },
                   p.l2norm, p.scale);
     if (tid < V) sm.v[tid] = vv_lds[j][tid];
-    const float decay = __expf(ldf<GT>(p.g, b * p.HV + hv));
-    const float beta = p.beta ? ldf<BT>(p.beta, b * p.HV + hv) : 1.0f;
+    float gv = ldf<GT>(p.g, b * p.HV + hv);
+    float beta = p.beta ? ldf<BT>(p.beta, b * p.HV + hv) : 1.0f;
+    if (p.gating) {
+      gv = gdn_log_decay(gv + p.dt_bias[hv], p.A_log[hv], p.sp_beta, p.sp_thr);
+      beta = sigmoid_exact(beta);
+    }
+    const float decay = __expf(gv);
     T* o = reinterpret_cast<T*>(p.o) + (b * p.HV + hv) * V;
     gdn_token<K, V>(t, sm, decay, beta, [&](int c, float val) { o[c] = from_f32<T>(val); });
     if (st_ok) store_tile<K, V>(t, sbase);
@@ -573,28 +664,31 @@ extern "C" int xk_gdn_recurrent(
   return XK_ERR_UNSUPPORTED;
 }
 
-extern "C" int xk_gdn_conv_decode(
-    const void* mixed_qkv, int64_t stride_x_row, void* conv_state,
-    int64_t stride_cs_line, int64_t stride_cs_dim, int64_t stride_cs_tok,
-    int64_t conv_lines, int64_t conv_state_len, const void* conv_weight,
-    int64_t stride_w_dim, int64_t stride_w_tap, const void* conv_bias,
-    xk_dtype w_dtype, int64_t width, const int32_t* conv_state_indices,
-    int32_t pad_slot_id, const void* g, xk_dtype g_dtype, const void* beta,
-    xk_dtype beta_dtype, float* ssm_state, int64_t stride_state_slot,
-    int64_t num_slots, const int32_t* ssm_state_indices, void* o, int64_t B,
-    int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
-    int use_qk_l2norm, xk_dtype dtype, void* stream) {
+namespace {
+
+// Shared argument checks and launch of the fused decode step; p.g / p.beta
+// (and, with p.gating, a / b) are already set.
+int conv_decode_launch(FusedParams& p, const void* mixed_qkv, int64_t stride_x_row,
+                       void* conv_state, int64_t stride_cs_line, int64_t stride_cs_dim,
+                       int64_t stride_cs_tok, int64_t conv_lines, int64_t conv_state_len,
+                       const void* conv_weight, int64_t stride_w_dim, int64_t stride_w_tap,
+                       const void* conv_bias, xk_dtype w_dtype, int64_t width,
+                       const int32_t* conv_state_indices, int32_t pad_slot_id, xk_dtype g_dtype,
+                       xk_dtype beta_dtype, float* ssm_state, int64_t stride_state_slot,
+                       int64_t num_slots, const int32_t* ssm_state_indices, void* o, int64_t B,
+                       int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+                       int use_qk_l2norm, xk_dtype dtype, void* stream) {
   if (B < 0 || H <= 0 || HV <= 0 || HV % H != 0 || HV / H > 16 || width < 1 ||
       conv_state_len < width - 1 || conv_state_len < 1)
     return XK_ERR_INVALID;
   if (!is_float_dtype(dtype) || !is_float_dtype(g_dtype) || !is_float_dtype(w_dtype) ||
-      (beta && !is_float_dtype(beta_dtype)))
+      (p.beta && !is_float_dtype(beta_dtype)))
     return XK_ERR_UNSUPPORTED;
   if (B == 0) return XK_OK;
-  if (!mixed_qkv || !conv_state || !conv_weight || !g || !ssm_state || !o)
+  if (!mixed_qkv || !conv_state || !conv_weight || !p.g || !ssm_state || !o)
     return XK_ERR_INVALID;
   if (!aligned(ssm_state, 16) || stride_state_slot % 4) return XK_ERR_INVALID;
-  FusedParams p{};
+  if (K != 128 || V != 128) return XK_ERR_UNSUPPORTED;
   p.x = mixed_qkv;
   p.sx = stride_x_row;
   p.conv_state = conv_state;
@@ -610,8 +704,6 @@ extern "C" int xk_gdn_conv_decode(
   p.wdt = w_dtype;
   p.conv_idx = conv_state_indices;
   p.W = static_cast<int>(width);
-  p.g = g;
-  p.beta = beta;
   p.state = ssm_state;
   p.st_slot_stride = stride_state_slot;
   p.slots = num_slots;
@@ -623,15 +715,73 @@ extern "C" int xk_gdn_conv_decode(
   p.scale = scale;
   p.l2norm = use_qk_l2norm;
   p.pad = pad_slot_id;
+  p.conv_vec = (dtype == XK_BF16 || dtype == XK_F16) && w_dtype == dtype &&
+               stride_w_dim == width && stride_w_tap == 1 && stride_cs_tok == 1 &&
+               stride_cs_dim == conv_state_len && conv_state_len == width - 1 &&
+               conv_state_len <= 4 && stride_cs_line % 8 == 0 && stride_x_row % 8 == 0 &&
+               aligned(mixed_qkv, 16) && aligned(conv_state, 16) && aligned(conv_weight, 16);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const xk_dtype bdt = beta ? beta_dtype : XK_F32;
-  if (K != 128 || V != 128) return XK_ERR_UNSUPPORTED;
+  const xk_dtype bdt = p.beta ? beta_dtype : XK_F32;
   switch (dtype) {
     case XK_BF16: return fused_g<128, 128, bf16>(p, g_dtype, bdt, s);
     case XK_F16: return fused_g<128, 128, f16>(p, g_dtype, bdt, s);
     case XK_F32: return fused_g<128, 128, float>(p, g_dtype, bdt, s);
     default: return XK_ERR_UNSUPPORTED;
   }
+}
+
+}  // namespace
+
+extern "C" int xk_gdn_conv_decode(
+    const void* mixed_qkv, int64_t stride_x_row, void* conv_state,
+    int64_t stride_cs_line, int64_t stride_cs_dim, int64_t stride_cs_tok,
+    int64_t conv_lines, int64_t conv_state_len, const void* conv_weight,
+    int64_t stride_w_dim, int64_t stride_w_tap, const void* conv_bias,
+    xk_dtype w_dtype, int64_t width, const int32_t* conv_state_indices,
+    int32_t pad_slot_id, const void* g, xk_dtype g_dtype, const void* beta,
+    xk_dtype beta_dtype, float* ssm_state, int64_t stride_state_slot,
+    int64_t num_slots, const int32_t* ssm_state_indices, void* o, int64_t B,
+    int64_t H, int64_t HV, int64_t K, int64_t V, float scale,
+    int use_qk_l2norm, xk_dtype dtype, void* stream) {
+  FusedParams p{};
+  p.g = g;
+  p.beta = beta;
+  return conv_decode_launch(p, mixed_qkv, stride_x_row, conv_state, stride_cs_line,
+                            stride_cs_dim, stride_cs_tok, conv_lines, conv_state_len,
+                            conv_weight, stride_w_dim, stride_w_tap, conv_bias, w_dtype, width,
+                            conv_state_indices, pad_slot_id, g_dtype, beta_dtype, ssm_state,
+                            stride_state_slot, num_slots, ssm_state_indices, o, B, H, HV, K, V,
+                            scale, use_qk_l2norm, dtype, stream);
+}
+
+extern "C" int xk_gdn_conv_gating_decode(
+    const void* mixed_qkv, int64_t stride_x_row, void* conv_state,
+    int64_t stride_cs_line, int64_t stride_cs_dim, int64_t stride_cs_tok,
+    int64_t conv_lines, int64_t conv_state_len, const void* conv_weight,
+    int64_t stride_w_dim, int64_t stride_w_tap, const void* conv_bias,
+    xk_dtype w_dtype, int64_t width, const int32_t* conv_state_indices,
+    int32_t pad_slot_id, const float* A_log, const void* a, const float* dt_bias,
+    const void* b, xk_dtype ab_dtype, float softplus_beta, float threshold,
+    float* ssm_state, int64_t stride_state_slot, int64_t num_slots,
+    const int32_t* ssm_state_indices, void* o, int64_t B, int64_t H, int64_t HV,
+    int64_t K, int64_t V, float scale, int use_qk_l2norm, xk_dtype dtype,
+    void* stream) {
+  if (B > 0 && (!A_log || !dt_bias || !a || !b)) return XK_ERR_INVALID;
+  if (softplus_beta == 0.f) return XK_ERR_INVALID;
+  FusedParams p{};
+  p.g = a;
+  p.beta = b;
+  p.gating = 1;
+  p.A_log = A_log;
+  p.dt_bias = dt_bias;
+  p.sp_beta = softplus_beta;
+  p.sp_thr = threshold;
+  return conv_decode_launch(p, mixed_qkv, stride_x_row, conv_state, stride_cs_line,
+                            stride_cs_dim, stride_cs_tok, conv_lines, conv_state_len,
+                            conv_weight, stride_w_dim, stride_w_tap, conv_bias, w_dtype, width,
+                            conv_state_indices, pad_slot_id, ab_dtype, ab_dtype, ssm_state,
+                            stride_state_slot, num_slots, ssm_state_indices, o, B, H, HV, K, V,
+                            scale, use_qk_l2norm, dtype, stream);
 }
 
 extern "C" int xk_fused_gdn_gating(const float* A_log, const void* a, const void* b,

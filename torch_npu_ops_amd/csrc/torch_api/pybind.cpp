@@ -73,6 +73,12 @@ PYBIND11_MODULE(_xk_torch, m) {
         "head_k"_a = 128, "head_v"_a = 128, "scale"_a = std::optional<float>(),
         "conv_bias"_a = OptT(), "conv_state_indices"_a = OptT(), "ssm_state_indices"_a = OptT(),
         "pad_slot_id"_a = -1, "use_qk_l2norm"_a = true);
+  m.def("npu_gdn_conv_sigmoid_gating_decode", &npu::npu_gdn_conv_sigmoid_gating_decode,
+        "mixed_qkv"_a, "conv_state"_a, "conv_weight"_a, "A_log"_a, "a"_a, "dt_bias"_a, "b"_a,
+        "ssm_state"_a, "num_heads_qk"_a, "num_heads_v"_a, "head_k"_a = 128, "head_v"_a = 128,
+        "scale"_a = std::optional<float>(), "conv_bias"_a = OptT(),
+        "conv_state_indices"_a = OptT(), "ssm_state_indices"_a = OptT(), "pad_slot_id"_a = -1,
+        "softplus_beta"_a = 1.0f, "softplus_threshold"_a = 20.0f, "use_qk_l2norm"_a = true);
   // npu_ops (AscendC API): gemma returns (rstd, y) for its two out-params.
   m.def("npu_ops_gemma_rms_norm", [](const torch::Tensor& x, const torch::Tensor& gamma,
                                      double eps) {

@@ -699,20 +699,19 @@ torch::Tensor npu_chunk_fwd_o(const torch::Tensor& q, const torch::Tensor& k,
   return o;
 }
 
-torch::Tensor npu_gdn_conv_decode(
-    torch::Tensor& mixed_qkv, torch::Tensor& conv_state, torch::Tensor& conv_weight,
-    torch::Tensor& g, const std::optional<torch::Tensor>& beta, torch::Tensor& ssm_state,
-    int64_t num_heads_qk, int64_t num_heads_v, int64_t head_k, int64_t head_v,
-    const std::optional<float>& scale, const std::optional<torch::Tensor>& conv_bias,
-    const std::optional<torch::Tensor>& conv_state_indices,
-    const std::optional<torch::Tensor>& ssm_state_indices, int32_t pad_slot_id,
-    bool use_qk_l2norm) {
+namespace {
+
+// Checks shared by the two fused decode steps: the kernels index ssm_state
+// as dense fp32 [slots, HV, K, V] (slot stride from stride(0)) and
+// conv_state in mixed_qkv's dtype.
+void check_conv_decode(const torch::Tensor& mixed_qkv, const torch::Tensor& conv_state,
+                       const torch::Tensor& conv_weight, const torch::Tensor& ssm_state,
+                       int64_t num_heads_qk, int64_t num_heads_v, int64_t head_k,
+                       int64_t head_v) {
   TORCH_CHECK(mixed_qkv.dim() == 2, "gdn_conv_decode expects mixed_qkv [B, D]");
-  const int64_t B = mixed_qkv.size(0), D = mixed_qkv.size(1);
+  const int64_t D = mixed_qkv.size(1);
   TORCH_CHECK(D == 2 * num_heads_qk * head_k + num_heads_v * head_v,
               "mixed_qkv width does not match the head layout");
-  // The kernels index ssm_state as dense fp32 [slots, HV, K, V] (slot stride
-  // from stride(0)) and conv_state in mixed_qkv's dtype.
   TORCH_CHECK(ssm_state.scalar_type() == torch::kFloat32, "ssm_state must be float32");
   TORCH_CHECK(ssm_state.dim() == 4 && ssm_state.size(1) == num_heads_v &&
                   ssm_state.size(2) == head_k && ssm_state.size(3) == head_v,
@@ -726,6 +725,21 @@ torch::Tensor npu_gdn_conv_decode(
               "conv_state must have shape [lines, D, state_len]");
   TORCH_CHECK(conv_weight.dim() == 2 && conv_weight.size(0) == D,
               "conv_weight must have shape [D, width]");
+}
+
+}  // namespace
+
+torch::Tensor npu_gdn_conv_decode(
+    torch::Tensor& mixed_qkv, torch::Tensor& conv_state, torch::Tensor& conv_weight,
+    torch::Tensor& g, const std::optional<torch::Tensor>& beta, torch::Tensor& ssm_state,
+    int64_t num_heads_qk, int64_t num_heads_v, int64_t head_k, int64_t head_v,
+    const std::optional<float>& scale, const std::optional<torch::Tensor>& conv_bias,
+    const std::optional<torch::Tensor>& conv_state_indices,
+    const std::optional<torch::Tensor>& ssm_state_indices, int32_t pad_slot_id,
+    bool use_qk_l2norm) {
+  check_conv_decode(mixed_qkv, conv_state, conv_weight, ssm_state, num_heads_qk, num_heads_v,
+                    head_k, head_v);
+  const int64_t B = mixed_qkv.size(0);
   TORCH_CHECK(g.dim() == 2 && g.size(0) == B && g.size(1) == num_heads_v,
               "g must have shape [B, num_heads_v]");
   TORCH_CHECK(!has(beta) || (beta->dim() == 2 && beta->size(0) == B &&
@@ -751,6 +765,50 @@ torch::Tensor npu_gdn_conv_decode(
                            o.data_ptr(), B, num_heads_qk, num_heads_v, head_k, head_v, sc,
                            use_qk_l2norm, xdt(x), stream_of(x)),
         "xk_gdn_conv_decode");
+  return o;
+}
+
+torch::Tensor npu_gdn_conv_sigmoid_gating_decode(
+    torch::Tensor& mixed_qkv, torch::Tensor& conv_state, torch::Tensor& conv_weight,
+    torch::Tensor& A_log, torch::Tensor& a, torch::Tensor& dt_bias, torch::Tensor& b,
+    torch::Tensor& ssm_state, int64_t num_heads_qk, int64_t num_heads_v, int64_t head_k,
+    int64_t head_v, const std::optional<float>& scale,
+    const std::optional<torch::Tensor>& conv_bias,
+    const std::optional<torch::Tensor>& conv_state_indices,
+    const std::optional<torch::Tensor>& ssm_state_indices, int32_t pad_slot_id,
+    float softplus_beta, float softplus_threshold, bool use_qk_l2norm) {
+  check_conv_decode(mixed_qkv, conv_state, conv_weight, ssm_state, num_heads_qk, num_heads_v,
+                    head_k, head_v);
+  const int64_t B = mixed_qkv.size(0);
+  TORCH_CHECK(a.dim() == 2 && a.size(0) == B && a.size(1) == num_heads_v,
+              "a must have shape [B, num_heads_v]");
+  TORCH_CHECK(b.sizes() == a.sizes(), "a/b shape mismatch");
+  TORCH_CHECK(a.scalar_type() == b.scalar_type(), "a and b must have the same dtype");
+  TORCH_CHECK(A_log.scalar_type() == torch::kFloat32 && A_log.numel() == num_heads_v,
+              "A_log must be float32 [num_heads_v]");
+  TORCH_CHECK(dt_bias.scalar_type() == torch::kFloat32 && dt_bias.numel() == num_heads_v,
+              "dt_bias must be float32 [num_heads_v]");
+  const float sc = scale.has_value() ? *scale : 1.0f / std::sqrt(static_cast<float>(head_k));
+  auto x = mixed_qkv.stride(1) == 1 ? mixed_qkv : mixed_qkv.contiguous();
+  torch::Tensor cb, ci, si;
+  if (has(conv_bias)) cb = conv_bias->to(conv_weight.scalar_type()).contiguous();
+  if (has(conv_state_indices)) ci = conv_state_indices->to(torch::kInt32).contiguous();
+  if (has(ssm_state_indices)) si = ssm_state_indices->to(torch::kInt32).contiguous();
+  auto ac = a.contiguous(), bc = b.contiguous();
+  auto al = A_log.contiguous(), db = dt_bias.contiguous();
+  auto o = torch::empty({B, num_heads_v, head_v}, x.options());
+  check(xk_gdn_conv_gating_decode(
+            x.data_ptr(), x.stride(0), conv_state.data_ptr(), conv_state.stride(0),
+            conv_state.stride(1), conv_state.stride(2), conv_state.size(0), conv_state.size(2),
+            conv_weight.data_ptr(), conv_weight.stride(0), conv_weight.stride(1), ptr(cb),
+            xdt(conv_weight), conv_weight.size(1), static_cast<const int32_t*>(ptr(ci)),
+            pad_slot_id, static_cast<const float*>(al.data_ptr()), ac.data_ptr(),
+            static_cast<const float*>(db.data_ptr()), bc.data_ptr(), xdt(ac), softplus_beta,
+            softplus_threshold, static_cast<float*>(ssm_state.data_ptr()), ssm_state.stride(0),
+            ssm_state.size(0), static_cast<const int32_t*>(ptr(si)), o.data_ptr(), B,
+            num_heads_qk, num_heads_v, head_k, head_v, sc, use_qk_l2norm, xdt(x),
+            stream_of(x)),
+        "xk_gdn_conv_gating_decode");
   return o;
 }
 

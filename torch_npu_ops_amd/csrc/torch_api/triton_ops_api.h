@@ -144,4 +144,19 @@ torch::Tensor npu_gdn_conv_decode(
     const std::optional<torch::Tensor>& ssm_state_indices = std::nullopt,
     int32_t pad_slot_id = -1, bool use_qk_l2norm = true);
 
+// The same decode step with the gating in the kernel: g = -exp(A_log) *
+// softplus(a + dt_bias) and beta = sigmoid(b) per (row, v head), as
+// npu_fused_sigmoid_gating_delta_rule_update forms them; a, b [B, Hv],
+// A_log, dt_bias fp32 [Hv].  One launch from the projection outputs.
+torch::Tensor npu_gdn_conv_sigmoid_gating_decode(
+    torch::Tensor& mixed_qkv, torch::Tensor& conv_state, torch::Tensor& conv_weight,
+    torch::Tensor& A_log, torch::Tensor& a, torch::Tensor& dt_bias, torch::Tensor& b,
+    torch::Tensor& ssm_state, int64_t num_heads_qk, int64_t num_heads_v, int64_t head_k = 128,
+    int64_t head_v = 128, const std::optional<float>& scale = std::nullopt,
+    const std::optional<torch::Tensor>& conv_bias = std::nullopt,
+    const std::optional<torch::Tensor>& conv_state_indices = std::nullopt,
+    const std::optional<torch::Tensor>& ssm_state_indices = std::nullopt,
+    int32_t pad_slot_id = -1, float softplus_beta = 1.0f, float softplus_threshold = 20.0f,
+    bool use_qk_l2norm = true);
+
 }  // namespace xllm::kernel::npu

@@ -799,18 +799,8 @@ def npu_chunk_fwd_o(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, h: torch.
     return o
 
 
-def gdn_conv_decode(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
-                    conv_weight: torch.Tensor, g: torch.Tensor,
-                    beta: Optional[torch.Tensor], ssm_state: torch.Tensor,
-                    num_heads_qk: int, num_heads_v: int, head_k: int = 128,
-                    head_v: int = 128, scale: Optional[float] = None,
-                    conv_bias: Optional[torch.Tensor] = None,
-                    conv_state_indices: Optional[torch.Tensor] = None,
-                    ssm_state_indices: Optional[torch.Tensor] = None,
-                    pad_slot_id: int = -1, use_qk_l2norm: bool = True):
-    """One fused decode step: conv1d update + SiLU of mixed_qkv [B, D],
-    split into q / k / v heads, l2norm, one gated-delta-rule step on
-    ssm_state (updated in place).  Returns o [B, HV, V]."""
+def _check_conv_decode(mixed_qkv, conv_state, conv_weight, ssm_state, num_heads_qk,
+                       num_heads_v, head_k, head_v):
     if mixed_qkv.dim() != 2:
         raise ValueError("gdn_conv_decode expects mixed_qkv [B, D]")
     B, D = mixed_qkv.shape
@@ -831,29 +821,96 @@ def gdn_conv_decode(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
         raise ValueError("conv_state must have shape [lines, D, state_len]")
     if conv_weight.dim() != 2 or conv_weight.size(0) != D:
         raise ValueError("conv_weight must have shape [D, width]")
-    if tuple(g.shape) != (B, num_heads_v):
-        raise ValueError("g must have shape [B, num_heads_v]")
-    if beta is not None and tuple(beta.shape) != (B, num_heads_v):
-        raise ValueError("beta must have shape [B, num_heads_v]")
-    sc = float(scale) if scale is not None else 1.0 / math.sqrt(head_k)
+    return B, D
+
+
+def _conv_decode_common(mixed_qkv, conv_state, conv_weight, ssm_state, conv_bias,
+                        conv_state_indices, ssm_state_indices, pad_slot_id, head_k):
+    """Leading C-ABI arguments shared by both fused decode entry points."""
     x = mixed_qkv if mixed_qkv.stride(1) == 1 else mixed_qkv.contiguous()
     w = conv_weight
     cb = conv_bias.to(w.dtype).contiguous() if conv_bias is not None else None
     ci = conv_state_indices.to(torch.int32).contiguous() if conv_state_indices is not None else None
     si = ssm_state_indices.to(torch.int32).contiguous() if ssm_state_indices is not None else None
+    head = (x.data_ptr(), x.stride(0), conv_state.data_ptr(), conv_state.stride(0),
+            conv_state.stride(1), conv_state.stride(2), conv_state.size(0),
+            conv_state.size(2), w.data_ptr(), w.stride(0), w.stride(1), _ptr(cb),
+            xk_dtype(w), w.size(1), _ptr(ci), int(pad_slot_id))
+    keep = (x, cb, ci, si)  # alive until the launch is enqueued
+    return x, head, si, keep
+
+
+def gdn_conv_decode(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
+                    conv_weight: torch.Tensor, g: torch.Tensor,
+                    beta: Optional[torch.Tensor], ssm_state: torch.Tensor,
+                    num_heads_qk: int, num_heads_v: int, head_k: int = 128,
+                    head_v: int = 128, scale: Optional[float] = None,
+                    conv_bias: Optional[torch.Tensor] = None,
+                    conv_state_indices: Optional[torch.Tensor] = None,
+                    ssm_state_indices: Optional[torch.Tensor] = None,
+                    pad_slot_id: int = -1, use_qk_l2norm: bool = True):
+    """One fused decode step: conv1d update + SiLU of mixed_qkv [B, D],
+    split into q / k / v heads, l2norm, one gated-delta-rule step on
+    ssm_state (updated in place).  Returns o [B, HV, V]."""
+    B, D = _check_conv_decode(mixed_qkv, conv_state, conv_weight, ssm_state, num_heads_qk,
+                              num_heads_v, head_k, head_v)
+    if tuple(g.shape) != (B, num_heads_v):
+        raise ValueError("g must have shape [B, num_heads_v]")
+    if beta is not None and tuple(beta.shape) != (B, num_heads_v):
+        raise ValueError("beta must have shape [B, num_heads_v]")
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(head_k)
+    x, head, si, _keep = _conv_decode_common(mixed_qkv, conv_state, conv_weight, ssm_state,
+                                              conv_bias, conv_state_indices,
+                                              ssm_state_indices, pad_slot_id, head_k)
     gc = g.contiguous()
     bc = beta.contiguous() if beta is not None else None
     o = torch.empty(B, num_heads_v, head_v, dtype=x.dtype, device=x.device)
     st = lib().xk_gdn_conv_decode(
-        x.data_ptr(), x.stride(0), conv_state.data_ptr(), conv_state.stride(0),
-        conv_state.stride(1), conv_state.stride(2), conv_state.size(0),
-        conv_state.size(2), w.data_ptr(), w.stride(0), w.stride(1), _ptr(cb),
-        xk_dtype(w), w.size(1), _ptr(ci), int(pad_slot_id), gc.data_ptr(),
-        xk_dtype(gc), _ptr(bc), xk_dtype(bc) if bc is not None else 0,
+        *head, gc.data_ptr(), xk_dtype(gc), _ptr(bc), xk_dtype(bc) if bc is not None else 0,
         ssm_state.data_ptr(), ssm_state.stride(0), ssm_state.size(0), _ptr(si),
         o.data_ptr(), B, num_heads_qk, num_heads_v, head_k, head_v, sc,
         int(use_qk_l2norm), xk_dtype(x), _stream(x))
     check(st, "xk_gdn_conv_decode")
+    return o
+
+
+def gdn_conv_gating_decode(mixed_qkv: torch.Tensor, conv_state: torch.Tensor,
+                           conv_weight: torch.Tensor, A_log: torch.Tensor, a: torch.Tensor,
+                           dt_bias: torch.Tensor, b: torch.Tensor, ssm_state: torch.Tensor,
+                           num_heads_qk: int, num_heads_v: int, head_k: int = 128,
+                           head_v: int = 128, scale: Optional[float] = None,
+                           conv_bias: Optional[torch.Tensor] = None,
+                           conv_state_indices: Optional[torch.Tensor] = None,
+                           ssm_state_indices: Optional[torch.Tensor] = None,
+                           pad_slot_id: int = -1, softplus_beta: float = 1.0,
+                           softplus_threshold: float = 20.0, use_qk_l2norm: bool = True):
+    """gdn_conv_decode with the gating in the kernel: g = -exp(A_log) *
+    softplus(a + dt_bias) and beta = sigmoid(b) per (row, v head), in fp32
+    (as npu_fused_sigmoid_gating_delta_rule_update forms them).  a, b
+    [B, HV]; A_log, dt_bias fp32 [HV].  Returns o [B, HV, V]."""
+    B, D = _check_conv_decode(mixed_qkv, conv_state, conv_weight, ssm_state, num_heads_qk,
+                              num_heads_v, head_k, head_v)
+    for t, name in ((a, "a"), (b, "b")):
+        if tuple(t.shape) != (B, num_heads_v):
+            raise ValueError(f"{name} must have shape [B, num_heads_v]")
+    if a.dtype != b.dtype:
+        raise ValueError("a and b must have the same dtype")
+    for t, name in ((A_log, "A_log"), (dt_bias, "dt_bias")):
+        if t.dtype != torch.float32 or t.numel() != num_heads_v:
+            raise ValueError(f"{name} must be float32 [num_heads_v]")
+    sc = float(scale) if scale is not None else 1.0 / math.sqrt(head_k)
+    x, head, si, _keep = _conv_decode_common(mixed_qkv, conv_state, conv_weight, ssm_state,
+                                              conv_bias, conv_state_indices,
+                                              ssm_state_indices, pad_slot_id, head_k)
+    ac, bc = a.contiguous(), b.contiguous()
+    al, db = A_log.contiguous(), dt_bias.contiguous()
+    o = torch.empty(B, num_heads_v, head_v, dtype=x.dtype, device=x.device)
+    st = lib().xk_gdn_conv_gating_decode(
+        *head, al.data_ptr(), ac.data_ptr(), db.data_ptr(), bc.data_ptr(), xk_dtype(ac),
+        float(softplus_beta), float(softplus_threshold), ssm_state.data_ptr(),
+        ssm_state.stride(0), ssm_state.size(0), _ptr(si), o.data_ptr(), B, num_heads_qk,
+        num_heads_v, head_k, head_v, sc, int(use_qk_l2norm), xk_dtype(x), _stream(x))
+    check(st, "xk_gdn_conv_gating_decode")
     return o
 
 
