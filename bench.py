@@ -1254,6 +1254,128 @@ def floors(dev, steps, warmup, moved_list):
     return out
 
 
+# ---------------------------------------------------------------------------
+# Profile summaries (profiles/): rocprofv3 output of the runs listed in
+# PROFILE_COMMANDS, summarised into the kernel-duration and HBM-traffic tables
+# and the traffic JSON that measured_traffic() reads.
+# ---------------------------------------------------------------------------
+PROFILE_COMMANDS = [
+    ("trace", "rocprofv3 --kernel-trace --stats -f csv -d <out>/trace -o run -- "
+              "python3 <repo>/bench.py --no-cpu"),
+    ("FETCH_SIZE", "rocprofv3 --pmc FETCH_SIZE -f csv -d <out>/FETCH_SIZE -o p -- "
+                   "python3 <repo>/bench.py --no-cpu --eager --steps 3 --warmup 1"),
+    ("WRITE_SIZE", "rocprofv3 --pmc WRITE_SIZE -f csv -d <out>/WRITE_SIZE -o p -- "
+                   "python3 <repo>/bench.py --no-cpu --eager --steps 3 --warmup 1"),
+    ("copy_FETCH_SIZE", "rocprofv3 --pmc FETCH_SIZE -f csv -d <out>/copy_FETCH_SIZE -o p -- "
+                        "python3 <repo>/bench.py --copy-calibration --steps 5"),
+    ("copy_WRITE_SIZE", "rocprofv3 --pmc WRITE_SIZE -f csv -d <out>/copy_WRITE_SIZE -o p -- "
+                        "python3 <repo>/bench.py --copy-calibration --steps 5"),
+]
+
+
+def kernel_label(raw):
+    """Short kernel name of a rocprofv3 kernel name (mangled or not): the
+    kernel identifier, with ln_tile_kernel's template arguments and
+    chunk_offsets_kernel's parameter type kept."""
+    import re
+    m = re.search(r"chunk_offsets_kernel<xk::\(anonymous namespace\)::(\w+)>", raw)
+    if m:
+        return f"chunk_offsets_kernel<{m.group(1)}>"
+    m = re.search(r"ln_tile_kernelI\w+?Li\d+ELi(\d+)ELi(\d+)ELb(\d)ELb(\d)E", raw)
+    if m:
+        return f"ln_tile_kernel<TPG={m.group(1)},NV={m.group(2)},z={m.group(3)}>"
+    m = re.search(r"\d+([a-z][a-z0-9_]*_kernel)I", raw)  # mangled template kernel
+    if m:
+        return m.group(1)
+    m = re.search(r"([a-z][a-z0-9_]*_kernel)\b", raw)
+    if m:
+        return m.group(1)
+    for pat in (r"(__amd_rocclr_copyBuffer)", r"(FillFunctor)", r"(arange)"):
+        m = re.search(pat, raw)
+        if m:
+            return m.group(1)
+    return raw[:50]
+
+
+def summarize_profile(out_dir):
+    """Writes profiles/kernel_durations_all_configs.md,
+    profiles/hbm_traffic_all_configs.md and TRAFFIC_JSON from the rocprofv3
+    output directories of PROFILE_COMMANDS under out_dir."""
+    import csv
+    import collections
+    import glob
+    stats = []
+    for r in csv.DictReader(open(os.path.join(out_dir, "trace", "run_kernel_stats.csv"))):
+        stats.append((kernel_label(r["Name"]), int(r["Calls"]), float(r["AverageNs"]) / 1e3,
+                      float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3))
+    stats.sort(key=lambda x: -x[2])
+
+    def pmc(sub, counter):
+        acc = collections.defaultdict(list)
+        for r in csv.DictReader(open(os.path.join(out_dir, sub, "p_counter_collection.csv"))):
+            if r["Counter_Name"] == counter:
+                acc[kernel_label(r["Kernel_Name"])].append(float(r["Counter_Value"]))
+        return {k: statistics.mean(v) for k, v in acc.items()}
+
+    fetch, write = pmc("FETCH_SIZE", "FETCH_SIZE"), pmc("WRITE_SIZE", "WRITE_SIZE")
+    cf, cw = pmc("copy_FETCH_SIZE", "FETCH_SIZE"), pmc("copy_WRITE_SIZE", "WRITE_SIZE")
+    copyk = max(cf, key=cf.get)
+    ff = COPY_BYTES / (cf[copyk] * 1024)
+    wf = COPY_BYTES / (cw[copyk] * 1024)
+    algo = {}  # kernel -> algorithmic bytes of the ops it runs alone
+    kernel_ops = collections.defaultdict(list)
+    for c in CASES.values():
+        kernel_ops[c.kernel].append(c.name)
+        algo.setdefault(c.kernel, []).append(c.algo_bytes)
+    traffic = {k: fetch[k] * 1024 * ff + write[k] * 1024 * wf
+               for k in fetch if k in write}
+    csrc = os.path.join(REPO, "torch_npu_ops_amd", "csrc")
+    sources = {os.path.basename(f): source_sha(os.path.basename(f))
+               for f in sorted(glob.glob(os.path.join(csrc, "*.hip")))}
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump({"fetch_factor": ff, "write_factor": wf, "sources": sources,
+                   "traffic_bytes": traffic}, f, indent=1)
+    prof = os.path.join(REPO, "profiles")
+    cmds = dict(PROFILE_COMMANDS)
+    with open(os.path.join(prof, "kernel_durations_all_configs.md"), "w") as f:
+        f.write("# Kernel durations, all BASELINE configs\n\nCommand (repo root on the GPU box; "
+                "`cd /tmp && export TMPDIR=/tmp` first):\n\n    " + cmds["trace"] + "\n\n"
+                "bench.py's default timing per op (clock-settle phase, warm-up, 3 x 50 timed "
+                "calls on buffer sets rotated past the Infinity Cache; small ops graph-replayed, "
+                "plus their same-traffic copies).  Averages are rocprofv3's per-dispatch kernel "
+                "durations over every dispatch, settle phase included.  Summarised by "
+                "`python3 bench.py --summarize-profile <out>`.\n\n"
+                "| kernel | calls | avg us | min us | max us | bench ops |\n|---|---|---|---|---|---|\n")
+        for k, c, a, mn, mx in stats:
+            f.write(f"| {k} | {c} | {a:.2f} | {mn:.2f} | {mx:.2f} | "
+                    f"{', '.join(kernel_ops.get(k, [])) or '-'} |\n")
+    with open(os.path.join(prof, "hbm_traffic_all_configs.md"), "w") as f:
+        f.write("# HBM traffic per dispatch vs algorithmic bytes, all BASELINE configs\n\n"
+                "Commands (repo root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first; "
+                "each counter in its own run):\n\n")
+        for key in ("FETCH_SIZE", "WRITE_SIZE", "copy_FETCH_SIZE", "copy_WRITE_SIZE"):
+            f.write("    " + cmds[key] + "\n")
+        f.write(f"\nCalibration: a plain {COPY_BYTES >> 20} MiB device copy (`{copyk}`) reads "
+                f"FETCH_SIZE = {cf[copyk]:.0f} KiB and WRITE_SIZE = {cw[copyk]:.0f} KiB per "
+                f"dispatch, so bytes = FETCH_SIZE x 1024 x {ff:.3f} + WRITE_SIZE x 1024 x "
+                f"{wf:.3f}.  Summarised by `python3 bench.py --summarize-profile <out>`, which "
+                "also writes hbm_traffic_all_configs.json with a hash of every kernel source; "
+                "bench.py reports a kernel's traffic only while its source is unchanged.  For "
+                "an op made of several kernels (gdn_chunk_prefill, gdn_chunk_staged) the ratio "
+                "compares one kernel's traffic with the whole op's algorithmic bytes.\n\n"
+                "| kernel | FETCH KiB | WRITE KiB | HBM MB | algorithmic MB (bench op) | "
+                "traffic / algorithmic |\n|---|---|---|---|---|---|\n")
+        for k, *_ in stats:
+            if k not in traffic:
+                continue
+            a = algo.get(k)
+            ratio = f"{traffic[k] / statistics.mean(a):.3f}" if a else "-"
+            alg = f"{statistics.mean(a) / 1e6:.1f} ({', '.join(kernel_ops[k])})" if a else "-"
+            f.write(f"| {k} | {fetch[k]:.0f} | {write[k]:.0f} | {traffic[k] / 1e6:.1f} | {alg} | "
+                    f"{ratio} |\n")
+    print(f"[bench] wrote profiles/ summaries from {out_dir}", file=sys.stderr)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1268,10 +1390,16 @@ def main():
     ap.add_argument("--floors", action="store_true",
                     help="only time the launch floor (empty kernel) and plain copies moving "
                          "the bytes of every small (graph-timed) op, and print them as JSON")
+    ap.add_argument("--summarize-profile", metavar="OUT",
+                    help="summarise the rocprofv3 output of PROFILE_COMMANDS under OUT into "
+                         "profiles/ (no GPU needed)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run plain 256 MiB device copies (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
+    if args.summarize_profile:
+        summarize_profile(args.summarize_profile)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); "
               "these ops are per-rank kernels with no collectives, so run it "

@@ -43,6 +43,10 @@ HIP_FLAGS = [
 ]
 
 
+# Per-source extra hipcc flags (none at present).
+EXTRA_FLAGS: dict[str, list[str]] = {}
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                           text=True)
@@ -69,7 +73,8 @@ def build_lib(jobs: int | None = None, verbose: bool = True) -> str:
 
     def compile_one(pair):
         src, obj = pair
-        _run([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+        _run([HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src,
+              "-o", obj])
         return obj
 
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
