@@ -82,6 +82,55 @@ def test_gating_large_batch(dev):
     _check_gating(dev, *_gating_inputs(4096, 32, torch.bfloat16, 8, dt_ones=False))
 
 
+def _every_bf16(lo, hi, heads=32):
+    """Every finite bf16 value in [lo, hi], padded with zeros to [rows, heads]."""
+    allv = torch.arange(0, 1 << 16, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    f = allv.float()
+    vals = allv[torch.isfinite(f) & (f >= lo) & (f <= hi)]
+    pad = (-vals.numel()) % heads
+    vals = torch.cat([vals, torch.zeros(pad, dtype=torch.bfloat16)])
+    return vals.reshape(-1, heads)
+
+
+def test_gating_softplus_accuracy_every_bf16(dev):
+    """g = -softplus(a) (A_log = 0, dt_bias = 0) for every bf16 a in
+    [-80, 60]: within 2e-6 relative of the float64 value, a tighter bound
+    than the reference's 1e-3; above the threshold g = -a exactly."""
+    from torch_npu_ops_amd import ops
+    a = _every_bf16(-80.0, 60.0)
+    heads = a.shape[1]
+    z = torch.zeros(heads)
+    g, _ = ops.npu_fused_gdn_gating(z.to(dev), a.to(dev), a.to(dev), z.to(dev), 1.0, 20.0)
+    g = g.cpu().double().reshape(a.shape)
+    x = a.double()
+    ref = -torch.where(x <= 20.0, torch.log1p(torch.exp(x)), x)
+    rel = ((g - ref).abs() / ref.abs().clamp_min(1e-300)).max().item()
+    assert rel <= 2e-6, rel
+    hi = x > 20.0
+    assert torch.equal(g[hi], -x[hi])
+
+
+def test_gating_beta_rounding_every_bf16(dev):
+    """beta = sigmoid(b) rounded to bf16 for every bf16 b in [-64, 64]
+    (both sides of the kernel's |b| < 32 fast path) equals the correctly
+    rounded sigmoid, except where the exact value lies within 4 fp32 ulp of
+    a bf16 rounding midpoint (there a 1-ulp fp32 evaluation may round
+    either way)."""
+    from torch_npu_ops_amd import ops
+    b = _every_bf16(-64.0, 64.0)
+    heads = b.shape[1]
+    z = torch.zeros(heads)
+    _, bo = ops.npu_fused_gdn_gating(z.to(dev), b.to(dev), b.to(dev), z.to(dev), 1.0, 20.0)
+    bo = bo.cpu().reshape(b.shape)
+    s32 = torch.sigmoid(b.double()).float()
+    low = s32.view(torch.int32) & 0xFFFF
+    near = (low - 0x8000).abs() <= 4
+    assert near.float().mean().item() < 1e-3
+    ref = s32.bfloat16()
+    ok = ~near
+    assert torch.equal(bo[ok].view(torch.int16), ref[ok].view(torch.int16))
+
+
 # ---------------------------------------------------------------------------
 def _update_inputs(B, T, H, HV, K, V, slots, seed):
     gen = torch.Generator().manual_seed(seed)

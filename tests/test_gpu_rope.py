@@ -149,9 +149,11 @@ def test_single_token_and_empty(dev):
 # sin / cos, odd pair counts (scalar-pair path), strided rows and the C++
 # drop-in.  Tolerance: bf16 rtol 1.6e-2 / atol 1e-2 (fp32: 1e-5); the
 # untouched prefix must be unchanged bit for bit.
-# (37, 12): the wave-per-token kernel's second pass over heads is partial.
+# (37, 12): the wave-per-token kernel's second pass over heads is partial;
+# 8 / 16 / 24 / 32 heads take its 1- to 4-pass forms with every row loaded
+# first, 40 heads its loop.
 @pytest.mark.parametrize("batch,head", [(1, 8), (4, 8), (8, 8), (1, 1), (4, 1), (8, 1),
-                                        (4096, 16), (37, 12)])
+                                        (4096, 16), (37, 12), (19, 24), (23, 32), (7, 40)])
 def test_rope_inplace_reference_cases(dev, batch, head):
     _check_rope_inplace(dev, (batch, head, 512), 64, torch.bfloat16, torch.bfloat16, batch + head)
 

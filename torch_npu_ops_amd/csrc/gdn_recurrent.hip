@@ -61,19 +61,71 @@ __device__ __forceinline__ float ldf(const void* p, int64_t i) {
   return to_f32(reinterpret_cast<const T*>(p)[i]);
 }
 
+// softplus(x) = max(x, 0) + log1p(e^-|x|) on the hardware exp2 / log2
+// (v_exp_f32, v_log_f32).  e^-|x| = 2^p (1 + p_lo ln 2) with p = fl(-|x|
+// log2 e) and p_lo its rounding error (one fma) plus the error of the
+// float log2 e, so the result stays within a few ulp for large |x| too;
+// log1p(u) = log(1 + u) * u / ((1 + u) - 1) (Goldberg's correction; (1 + u)
+// - 1 is exact, and 1 + u == 1 gives u).  About 20 instructions against
+// ~100 for log1pf(expf(x)).
+__device__ __forceinline__ float softplus_hw(float x) {
+  constexpr float kLog2e = 1.44269502162933349609375f;  // float(log2 e)
+  constexpr float kLog2eLo = 1.925963e-08f;              // log2 e - kLog2e
+  constexpr float kLn2 = 0.693147180559945309f;
+  const float t = -fabsf(x);
+  const float p = t * kLog2e;
+  const float plo = fmaf(t, kLog2e, -p) + t * kLog2eLo;
+  const float u0 = __builtin_amdgcn_exp2f(p);
+  const float u = fmaf(u0, plo * kLn2, u0);
+  const float w = 1.f + u;
+  const float d = w - 1.f;
+  const float lp = d == 0.f ? u : __builtin_amdgcn_logf(w) * kLn2 * (u * __builtin_amdgcn_rcpf(d));
+  return fmaxf(x, 0.f) + lp;
+}
+
 // GDN gating (triton_src/test_fused_gdn_gating.py:30-43): the log-decay
 // g = -exp(A_log) * softplus_{beta, threshold}(a + dt_bias), where softplus
-// is log(1 + exp(beta x)) / beta below the threshold and x above it.
+// is log(1 + exp(beta x)) / beta below the threshold and x above it.  Both
+// exponentials use the hardware exp2 (exp(A_log) to ~1e-7 |A_log|
+// relative): g is fp32 and the reference's test holds it to rtol / atol
+// 1e-3 (test_fused_gdn_gating.py:107); the error here is below 1e-6.
+// inv_beta is 1 / sp_beta, multiplied in as the reference does.
 __device__ __forceinline__ float gdn_log_decay(float a_plus_bias, float A_log, float sp_beta,
-                                               float threshold) {
+                                               float inv_beta, float threshold) {
+  constexpr float kLog2e = 1.44269504088896341f;
   const float bx = sp_beta * a_plus_bias;
-  const float sp = bx <= threshold ? log1pf(expf(bx)) / sp_beta : a_plus_bias;
-  return -expf(A_log) * sp;
+  const float sp = bx <= threshold ? inv_beta * softplus_hw(bx) : a_plus_bias;
+  return -__builtin_amdgcn_exp2f(A_log * kLog2e) * sp;
 }
 
 // sigmoid with IEEE division and the accurate exp, so that a rounded
 // 16-bit result matches a CPU computation of the same expression.
 __device__ __forceinline__ float sigmoid_exact(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// sigmoid(x) rounded to bf16, equal to sigmoid_exact's rounding.  For
+// |x| < 32 the hardware exp2 / rcp value is within about 50 fp32 ulp of
+// sigmoid_exact's: fl(-x log2 e) (< 64 in magnitude) is off by at most
+// 2^-19 for its rounding plus 32 * 2^-24 for the float log2 e, i.e. 2^-18,
+// which is 44 ulp of exp2 at most; exp2, the add, rcp and sigmoid_exact
+// itself add a few more.  So when the fast value's low 16 bits are more than
+// 128 from the bf16 rounding boundary 0x8000, both round to the same bf16.
+// Elsewhere (0.4% of values, and |x| >= 32 or NaN) sigmoid_exact is used.
+__device__ __forceinline__ bf16 sigmoid_bf16(float x) {
+  constexpr float kLog2e = 1.44269504088896341f;
+  float s = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
+  const uint32_t low = __builtin_bit_cast(uint32_t, s) & 0xFFFFu;
+  if (!(fabsf(x) < 32.f) || (low > 0x8000u - 128u && low < 0x8000u + 128u)) s = sigmoid_exact(x);
+  return from_f32<bf16>(s);
+}
+
+template <typename AB>
+__device__ __forceinline__ AB sigmoid_to(float x) {
+  if constexpr (std::is_same<AB, bf16>::value) {
+    return sigmoid_bf16(x);
+  } else {
+    return from_f32<AB>(sigmoid_exact(x));
+  }
+}
 
 // One token of the recurrence on the register tile.  Inputs (q, k already
 // normalised and q scaled) are in sm.q / sm.k / sm.v.  Writes o[V] through
@@ -289,7 +341,8 @@ __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
     r.g = ldf<GT>(p.g, tok * p.HV + hv);
     r.b = p.beta ? ldf<BT>(p.beta, tok * p.HV + hv) : 1.0f;
     if (p.gating) {
-      r.g = gdn_log_decay(r.g + p.dt_bias[hv], p.A_log[hv], p.sp_beta, p.sp_thr);
+      r.g = gdn_log_decay(r.g + p.dt_bias[hv], p.A_log[hv], p.sp_beta, 1.0f / p.sp_beta,
+                          p.sp_thr);
       r.b = sigmoid_exact(r.b);
     }
     return r;
@@ -370,34 +423,26 @@ int rec_t(const RecParams& p, xk_dtype dt, xk_dtype gdt, xk_dtype bdt, hipStream
 }
 
 // ---------------------------------------------------------------------------
-// GDN gating, elementwise over [rows, heads]: VEC consecutive elements per
-// lane.  Each element costs four transcendentals, so one element per lane
-// (the most lanes in flight) measured fastest on MI355X: 5.1 us for 16384 x
-// 32 elements, against 7.1 us with 8-element vectors.
+// GDN gating, elementwise over [rows, heads], one element per lane (the
+// most lanes in flight: every wave makes one load-compute-store pass, so the
+// compute is on each wave's critical path and more elements per lane only
+// lengthen it).  IT is the index type: 32-bit below 2^31 elements.
 // ---------------------------------------------------------------------------
-template <typename AB, int VEC>
+template <typename AB, typename IT>
 __global__ void __launch_bounds__(256)
     gdn_gating_kernel(const float* __restrict__ A_log, const AB* __restrict__ a,
                       const AB* __restrict__ b, const float* __restrict__ dt_bias,
-                      float* __restrict__ g, AB* __restrict__ beta_out, int64_t n,
-                      int heads, float sp_beta, float threshold) {
-  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * VEC;
-  if (i0 >= n) return;
-  using VA = Vec<AB, VEC>;
-  using VG = Vec<float, VEC>;
-  const VA av = ld_stream(reinterpret_cast<const VA*>(a + i0));
-  const VA bv = ld_stream(reinterpret_cast<const VA*>(b + i0));
-  VG gv;
-  VA ov;
-  int h = static_cast<int>(i0 % heads);
-#pragma unroll
-  for (int u = 0; u < VEC; ++u) {
-    gv.v[u] = gdn_log_decay(to_f32(av.v[u]) + dt_bias[h], A_log[h], sp_beta, threshold);
-    ov.v[u] = from_f32<AB>(sigmoid_exact(to_f32(bv.v[u])));
-    h = h + 1 == heads ? 0 : h + 1;
-  }
-  st_stream(reinterpret_cast<VG*>(g + i0), gv);
-  st_stream(reinterpret_cast<VA*>(beta_out + i0), ov);
+                      float* __restrict__ g, AB* __restrict__ beta_out, IT n, int heads,
+                      float sp_beta, float inv_beta, float threshold) {
+  const IT i = static_cast<IT>(blockIdx.x) * 256 + static_cast<IT>(threadIdx.x);
+  if (i >= n) return;
+  const AB av = ld_stream(a + i);
+  const AB bv = ld_stream(b + i);
+  // A power-of-two head count (the common case) is a mask, not a division.
+  const int h = (heads & (heads - 1)) == 0 ? static_cast<int>(i & static_cast<IT>(heads - 1))
+                                           : static_cast<int>(i % static_cast<IT>(heads));
+  st_stream(g + i, gdn_log_decay(to_f32(av) + dt_bias[h], A_log[h], sp_beta, inv_beta, threshold));
+  st_stream(beta_out + i, sigmoid_to<AB>(to_f32(bv)));
 }
 
 // ---------------------------------------------------------------------------
@@ -576,7 +621,7 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
     float gv = ldf<GT>(p.g, b * p.HV + hv);
     float beta = p.beta ? ldf<BT>(p.beta, b * p.HV + hv) : 1.0f;
     if (p.gating) {
-      gv = gdn_log_decay(gv + p.dt_bias[hv], p.A_log[hv], p.sp_beta, p.sp_thr);
+      gv = gdn_log_decay(gv + p.dt_bias[hv], p.A_log[hv], p.sp_beta, 1.0f / p.sp_beta, p.sp_thr);
       beta = sigmoid_exact(beta);
     }
     const float decay = __expf(gv);
@@ -804,15 +849,23 @@ extern "C" int xk_fused_gdn_gating(const float* A_log, const void* a, const void
   const int64_t n = rows * heads;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int hh = static_cast<int>(heads);
-#define XK_GATE(T, VEC)                                                                     \
-  hipLaunchKernelGGL((gdn_gating_kernel<T, VEC>), dim3(cdiv(n, 256 * VEC)), dim3(256), 0, s, \
-                     A_log, static_cast<const T*>(a), static_cast<const T*>(b), dt_bias,    \
-                     g_out, static_cast<T*>(beta_out), n, hh, softplus_beta, threshold)
-  switch (ab_dtype) {
-    case XK_BF16: XK_GATE(bf16, 1); break;
-    case XK_F16: XK_GATE(f16, 1); break;
-    default: XK_GATE(float, 1); break;
+#define XK_GATE(T, IT)                                                                       \
+  hipLaunchKernelGGL((gdn_gating_kernel<T, IT>), dim3(cdiv(n, 256)), dim3(256), 0, s, A_log,   \
+                     static_cast<const T*>(a), static_cast<const T*>(b), dt_bias, g_out,        \
+                     static_cast<T*>(beta_out), static_cast<IT>(n), hh, softplus_beta,          \
+                     1.0f / softplus_beta, threshold)
+#define XK_GATE_T(T)                                   \
+  if (n + 256 < (int64_t{1} << 31)) {                  \
+    XK_GATE(T, uint32_t);                              \
+  } else {                                             \
+    XK_GATE(T, int64_t);                               \
   }
+  switch (ab_dtype) {
+    case XK_BF16: XK_GATE_T(bf16); break;
+    case XK_F16: XK_GATE_T(f16); break;
+    default: XK_GATE_T(float); break;
+  }
+#undef XK_GATE_T
 #undef XK_GATE
   return launch_status();
 }

@@ -371,7 +371,11 @@ __global__ void __launch_bounds__(256)
 // One wave per token (vector path, rope_dim / VEC lanes per row dividing
 // the wave): each lane loads its sin/cos vectors once and rotates the same
 // slice of every head of the token, with a pass per 64 / lanes-per-row heads.
-template <typename T, typename A, int VEC, int LPR>
+// NP > 0: the token has exactly NP passes, and every pass's row is loaded
+// before the first store (NP rows in flight per lane; with a runtime pass
+// count the loop runs load-store, load-store).  That took the bench shape
+// (16 heads, 2 passes) from 17.4 to 17.1 us on MI355X.
+template <typename T, typename A, int VEC, int LPR, int NP>
 __global__ void __launch_bounds__(256)
     rope_inplace_tok_kernel(T* __restrict__ x, const A* __restrict__ sin,
                             const A* __restrict__ cos, int64_t tokens, int head_num, int64_t sx,
@@ -383,11 +387,7 @@ __global__ void __launch_bounds__(256)
   const int e0 = (ln % LPR) * VEC;
   using VT = Vec<T, VEC>;
   using VA = Vec<A, VEC>;
-  const VA sv = *reinterpret_cast<const VA*>(sin + tok * ssc + e0);
-  const VA cv = *reinterpret_cast<const VA*>(cos + tok * ssc + e0);
-  for (int h = ln / LPR; h < head_num; h += kRpp) {
-    T* xp = x + (tok * head_num + h) * sx + off + e0;
-    const VT xv = *reinterpret_cast<const VT*>(xp);
+  auto rotate = [&](const VT& xv, const VA& sv, const VA& cv) {
     VT ov;
 #pragma unroll
     for (int u = 0; u < VEC; u += 2) {
@@ -395,7 +395,27 @@ __global__ void __launch_bounds__(256)
       ov.v[u] = from_f32<T>(x0 * to_f32(cv.v[u]) - x1 * to_f32(sv.v[u]));
       ov.v[u + 1] = from_f32<T>(x1 * to_f32(cv.v[u + 1]) + x0 * to_f32(sv.v[u + 1]));
     }
-    *reinterpret_cast<VT*>(xp) = ov;
+    return ov;
+  };
+  if constexpr (NP > 0) {
+    VT xv[NP];
+    T* xp[NP];
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      xp[j] = x + (tok * head_num + ln / LPR + j * kRpp) * sx + off + e0;
+      xv[j] = *reinterpret_cast<const VT*>(xp[j]);
+    }
+    const VA sv = *reinterpret_cast<const VA*>(sin + tok * ssc + e0);
+    const VA cv = *reinterpret_cast<const VA*>(cos + tok * ssc + e0);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) *reinterpret_cast<VT*>(xp[j]) = rotate(xv[j], sv, cv);
+  } else {
+    const VA sv = *reinterpret_cast<const VA*>(sin + tok * ssc + e0);
+    const VA cv = *reinterpret_cast<const VA*>(cos + tok * ssc + e0);
+    for (int h = ln / LPR; h < head_num; h += kRpp) {
+      T* xp = x + (tok * head_num + h) * sx + off + e0;
+      *reinterpret_cast<VT*>(xp) = rotate(*reinterpret_cast<const VT*>(xp), sv, cv);
+    }
   }
 }
 
@@ -418,8 +438,18 @@ int launch_rope_inplace(void* x, const void* sin, const void* cos, int64_t rows,
   // Whole tokens (rows = tokens x head_num) with 8 lanes per row.
   if (vec && lanes == 8 && rows % head_num == 0) {
     const int64_t tokens = rows / head_num;
-    hipLaunchKernelGGL((rope_inplace_tok_kernel<T, A, kV, 8>), dim3(cdiv(tokens, 4)), dim3(256), 0,
-                       s, xp, sp, cp, tokens, head_num, sx, ssc, off);
+    const dim3 tg(cdiv(tokens, 4));
+#define XK_ROPE_TOK(NP) \
+  hipLaunchKernelGGL((rope_inplace_tok_kernel<T, A, kV, 8, NP>), tg, dim3(256), 0, s, xp, sp, cp, \
+                     tokens, head_num, sx, ssc, off)
+    switch (head_num % 8 ? 0 : head_num / 8) {
+      case 1: XK_ROPE_TOK(1); break;
+      case 2: XK_ROPE_TOK(2); break;
+      case 3: XK_ROPE_TOK(3); break;
+      case 4: XK_ROPE_TOK(4); break;
+      default: XK_ROPE_TOK(0); break;
+    }
+#undef XK_ROPE_TOK
     return launch_status();
   }
   if (vec)
