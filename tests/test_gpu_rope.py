@@ -130,6 +130,32 @@ def test_token_kernel(dev, hd, dtype, aux, mode):
     _check(out, ref, dtype)
 
 
+# Team kernel (under 1024 tokens): teams of 2 heads when both head counts
+# are even, else 1; 301 tokens leave a partial last block.
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (12, 4), (6, 2), (10, 2), (5, 1), (3, 3)])
+@pytest.mark.parametrize("mode", ["positions", "table"])
+def test_team_kernel_head_groups(dev, hq, hkv, mode):
+    from torch_npu_ops_amd import ops
+    T, hd = 301, 128
+    qkv, qw, kw, pos, inv, cos, sin = _case(T, hq, hkv, hd, torch.bfloat16, hq + hkv)
+    g = torch.Generator().manual_seed(13)
+    qb = torch.randn(hd, generator=g).bfloat16()
+    kb = torch.randn(hd, generator=g).bfloat16()
+    if mode == "positions":
+        cos, sin = orp.neox_cos_sin(pos, inv)
+    ref = orp.split_rmsnorm_rope(qkv, sin, cos, qw, kw, hq * hd, hkv * hd, hd, 1e-6,
+                                 q_bias=qb, k_bias=kb)
+    kw_ = dict(q_bias=qb.to(dev), k_bias=kb.to(dev), bias=True)
+    if mode == "positions":
+        out = ops.npu_split_rmsnorm_rope(qkv.to(dev), None, None, qw.to(dev), kw.to(dev),
+                                         hq * hd, hkv * hd, hd, 1e-6, positions=pos.to(dev),
+                                         inv_freq=inv.to(dev), **kw_)
+    else:
+        out = ops.npu_split_rmsnorm_rope(qkv.to(dev), sin.to(dev), cos.to(dev), qw.to(dev),
+                                         kw.to(dev), hq * hd, hkv * hd, hd, 1e-6, **kw_)
+    _check(out, ref, torch.bfloat16)
+
+
 def test_single_token_and_empty(dev):
     from torch_npu_ops_amd import ops
     qkv, qw, kw, pos, inv, cos, sin = _case(1, 4, 4, 128, torch.bfloat16, 4)

@@ -13,11 +13,12 @@
 // interface) or computed in registers from integer positions and an fp32
 // inverse-frequency table (neox layout: cos[d] = cos[d + half]).
 //
-// Design: one team of HALF/VEC lanes per (token, head).  Lane l holds the
-// VEC-element slices [l*VEC, l*VEC+VEC) and [half + l*VEC, ...) of the
-// head, so the rotate-half pairs (d, d + half) sit in the same lane and the
-// rotation needs no data exchange.  The head's sum of squares is a shuffle
-// reduction over the team; every global access is a 16-byte vector.
+// Design: one team of HALF/VEC lanes per (token, pair of heads) below 1024
+// tokens, one wave per token from there.  Lane l holds the VEC-element
+// slices [l*VEC, l*VEC+VEC) and [half + l*VEC, ...) of a head, so the
+// rotate-half pairs (d, d + half) sit in the same lane and the rotation
+// needs no data exchange.  A head's sum of squares is a shuffle reduction
+// over the team; every global access is a 16-byte vector.
 #include <type_traits>
 
 #include "xk_common.h"
@@ -69,7 +70,17 @@ __device__ __forceinline__ void st_f32(T* p, const float (&in)[N]) {
   st_stream(reinterpret_cast<Vec<T, N>*>(p), v);
 }
 
-template <typename T, typename A, int HD>
+// One team of HALF/VEC lanes per (token, group of G heads of one kind: all
+// q, all k or all v; the host checks that G divides both head counts).  The
+// team loads its cos/sin slice and weights once for its G heads.  Measured
+// on MI355X at config 1 (256 tokens, fp32), against 5.0 us for one head per
+// team: without the cos/sin and weight loads the kernel took 3.7 us (they
+// were three times the x loads in vector-memory instructions); G = 2 takes
+// 4.15 us, G = 4 4.5 us (half the waves, each twice as long); staging the
+// block's cos/sin rows and weights in LDS instead (one small load per lane
+// and a barrier) took 4.7-4.9 us.  Issuing the x loads first, before the
+// q / k / v branch, was worth 0.5 us of the G = 2 gain.
+template <typename T, typename A, int HD, int G>
 __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
   constexpr int kHalf = HD / 2;
   constexpr int kVec = (16 / sizeof(T)) < kHalf ? (16 / sizeof(T)) : kHalf;
@@ -79,39 +90,44 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
 
   const int team = threadIdx.x / kTeam;
   const int lane = threadIdx.x % kTeam;
-  const int heads = p.hq + 2 * p.hkv;
+  const int groups = (p.hq + 2 * p.hkv) / G;
   const int64_t slot = static_cast<int64_t>(blockIdx.x) * kTeams + team;
-  if (slot >= p.T * heads) return;  // whole team exits together
-  const int64_t tok = slot / heads;
-  const int h = static_cast<int>(slot - tok * heads);
+  if (slot >= p.T * groups) return;  // whole team exits together
+  const int64_t tok = slot / groups;
+  const int h = static_cast<int>(slot - tok * groups) * G;  // first head of the group
   const int d0 = lane * kVec;
 
   const T* row = reinterpret_cast<const T*>(p.qkv) + tok * p.stride_row;
   using VT = Vec<T, kVec>;
   using VA = Vec<A, kVec>;
-  if (h >= p.hq + p.hkv) {  // v: copy through
-    const int hv = h - p.hq - p.hkv;
-    const T* src = row + p.q_hidden + p.kv_hidden + static_cast<int64_t>(hv) * HD;
-    T* dst = reinterpret_cast<T*>(p.v) + tok * p.kv_hidden + static_cast<int64_t>(hv) * HD;
-    const VT a = ld_stream(reinterpret_cast<const VT*>(src + d0));
-    const VT c = ld_stream(reinterpret_cast<const VT*>(src + kHalf + d0));
-    st_stream(reinterpret_cast<VT*>(dst + d0), a);
-    st_stream(reinterpret_cast<VT*>(dst + kHalf + d0), c);
+  const bool is_v = h >= p.hq + p.hkv;
+  const bool is_q = h < p.hq;
+  const int hh = is_v ? h - p.hq - p.hkv : (is_q ? h : h - p.hq);
+  const T* src = row + (is_v ? p.q_hidden + p.kv_hidden : (is_q ? 0 : p.q_hidden)) +
+                 static_cast<int64_t>(hh) * HD;
+  VT xa[G], xb[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    xa[g] = ld_stream(reinterpret_cast<const VT*>(src + g * HD + d0));
+    xb[g] = ld_stream(reinterpret_cast<const VT*>(src + g * HD + kHalf + d0));
+  }
+  if (is_v) {  // v: copy through
+    T* dst = reinterpret_cast<T*>(p.v) + tok * p.kv_hidden + static_cast<int64_t>(hh) * HD;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      st_stream(reinterpret_cast<VT*>(dst + g * HD + d0), xa[g]);
+      st_stream(reinterpret_cast<VT*>(dst + g * HD + kHalf + d0), xb[g]);
+    }
     return;
   }
-  const bool is_q = h < p.hq;
-  const int hh = is_q ? h : h - p.hq;
-  const T* src = row + (is_q ? 0 : p.q_hidden) + static_cast<int64_t>(hh) * HD;
   T* dst = reinterpret_cast<T*>(is_q ? p.q : p.k) +
            tok * (is_q ? p.q_hidden : p.kv_hidden) + static_cast<int64_t>(hh) * HD;
-  const A* w = reinterpret_cast<const A*>(is_q ? p.qw : p.kw);
   const A* b = reinterpret_cast<const A*>(is_q ? p.qb : p.kb);
 
-  // Every load of the item is issued before the first use, so the kernel
+  // Every load of the group is issued before the first use, so the kernel
   // pays one memory latency: x (streamed), then weights, bias and sin/cos
-  // (shared by many items, served from cache).
-  const VT xa = ld_stream(reinterpret_cast<const VT*>(src + d0));
-  const VT xb = ld_stream(reinterpret_cast<const VT*>(src + kHalf + d0));
+  // (shared by many teams, served from cache).
+  const A* w = reinterpret_cast<const A*>(is_q ? p.qw : p.kw);
   const VA wa = *reinterpret_cast<const VA*>(w + d0);
   const VA wb = *reinterpret_cast<const VA*>(w + kHalf + d0);
   // Without a bias (the usual case) no bias loads are issued: the branch is
@@ -135,22 +151,6 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
     sb = *reinterpret_cast<const VA*>(sn + kHalf + d0);
   }
 
-  float x1[kVec], x2[kVec];
-  vec_f32(xa, x1);
-  vec_f32(xb, x2);
-  float ss = 0.f;
-#pragma unroll
-  for (int u = 0; u < kVec; ++u) ss = fmaf(x1[u], x1[u], fmaf(x2[u], x2[u], ss));
-  ss = group_sum<kTeam>(ss);
-  const float r = 1.0f / sqrtf(ss * (1.0f / HD) + p.eps);
-
-  float n1[kVec], n2[kVec];
-#pragma unroll
-  for (int u = 0; u < kVec; ++u) {
-    n1[u] = fmaf(x1[u] * r, to_f32(wa.v[u]), ba_f[u]);
-    n2[u] = fmaf(x2[u] * r, to_f32(wb.v[u]), bb_f[u]);
-  }
-
   float c1[kVec], c2[kVec], s1[kVec], s2[kVec];
   if (p.pos) {
     const float pos = p.pos_is_i64
@@ -170,14 +170,28 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
     vec_f32(sa, s1);
     vec_f32(sb, s2);
   }
-  float o1[kVec], o2[kVec];
+
 #pragma unroll
-  for (int u = 0; u < kVec; ++u) {
-    o1[u] = n1[u] * c1[u] - n2[u] * s1[u];
-    o2[u] = n2[u] * c2[u] + n1[u] * s2[u];
+  for (int g = 0; g < G; ++g) {
+    float x1[kVec], x2[kVec];
+    vec_f32(xa[g], x1);
+    vec_f32(xb[g], x2);
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) ss = fmaf(x1[u], x1[u], fmaf(x2[u], x2[u], ss));
+    ss = group_sum<kTeam>(ss);
+    const float r = 1.0f / sqrtf(ss * (1.0f / HD) + p.eps);
+    float o1[kVec], o2[kVec];
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      const float n1 = fmaf(x1[u] * r, to_f32(wa.v[u]), ba_f[u]);
+      const float n2 = fmaf(x2[u] * r, to_f32(wb.v[u]), bb_f[u]);
+      o1[u] = n1 * c1[u] - n2 * s1[u];
+      o2[u] = n2 * c2[u] + n1 * s2[u];
+    }
+    st_f32<T, kVec>(dst + g * HD + d0, o1);
+    st_f32<T, kVec>(dst + g * HD + kHalf + d0, o2);
   }
-  st_f32<T, kVec>(dst + d0, o1);
-  st_f32<T, kVec>(dst + kHalf + d0, o2);
 }
 
 // One wave per token.  The wave's 64 / kTeam teams take the token's heads
@@ -288,9 +302,9 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_tok_kernel(RopeParams 
   }
 }
 
-// Tokens from which the wave-per-token kernel is used: below it, one team
-// per (token, head) gives the launch more waves to spread over the 256 CUs
-// (at 256 tokens: 5.3 us against 12.7 us).
+// Tokens from which the wave-per-token kernel is used: below it, a team per
+// (token, head pair) gives the launch more waves to spread over the 256 CUs
+// (at 256 tokens, one team per head took 5.3 us against 12.7 us).
 constexpr int64_t kRopeTokKernelMin = 1024;
 
 template <typename T, typename A, int HD>
@@ -308,9 +322,17 @@ int launch_rope(const RopeParams& p, hipStream_t s) {
   constexpr int kHalf = HD / 2;
   constexpr int kVec = (16 / sizeof(T)) < kHalf ? (16 / sizeof(T)) : kHalf;
   constexpr int kTeams = 256 / (kHalf / kVec);
-  const int64_t slots = p.T * (p.hq + 2 * p.hkv);
-  hipLaunchKernelGGL((split_rmsnorm_rope_kernel<T, A, HD>), dim3(cdiv(slots, kTeams)),
-                     dim3(256), 0, s, p);
+  const int heads = p.hq + 2 * p.hkv;
+#define XK_ROPE_G(G)                                                                  \
+  hipLaunchKernelGGL((split_rmsnorm_rope_kernel<T, A, HD, G>),                        \
+                     dim3(cdiv(p.T * (heads / (G)), kTeams)), dim3(256), 0, s, p)
+  // Two heads per team when both head counts are even, else one.
+  if (p.hq % 2 == 0 && p.hkv % 2 == 0) {
+    XK_ROPE_G(2);
+  } else {
+    XK_ROPE_G(1);
+  }
+#undef XK_ROPE_G
   return launch_status();
 }
 
