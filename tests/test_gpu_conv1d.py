@@ -27,10 +27,11 @@ def _rn(shape, g, dtype, scale=1.0):
 
 # -- update (decode) ---------------------------------------------------------
 @pytest.mark.parametrize("bs", [1, 2, 4, 8, 16])
-@pytest.mark.parametrize("dim", [2048, 5120])
+@pytest.mark.parametrize("dim", [2048, 5120, 2056, 200])
 def test_update_reference_cases(dev, bs, dim):
     # test_causal_conv1d_update.py:1213-1255: bf16, width 4, seqlen 1, SiLU,
-    # no bias, indices arange.
+    # no bias, indices arange.  2056 and 200 channels end in a partial wave
+    # (64 lanes x 8 channels), which keeps direct per-lane state accesses.
     from torch_npu_ops_amd import ops
     g = torch.Generator().manual_seed(bs * 7 + dim)
     x = _rn((bs, dim, 1), g, torch.bfloat16)
