@@ -52,17 +52,22 @@ using namespace gdn;
 constexpr int kBVMax = 64;  // most V columns per P2 block (32 or 64)
 constexpr int kTh = 256;  // threads per block
 // Per-(chunk, head) record: ai_hi, ai_lo, aq, then the per-token factors
-// (fp32 [5][64]: cq, ck, b, ed, exp(gc_last)).  The three matrices are lower
-// triangular, so their zero upper-right 32 x 32 block is not stored: rows
-// 0..31 hold columns 0..31 (32 per row), rows 32..63 all 64 (tri_off).
-constexpr int kMat = (32 * 32 + 32 * 64) * 2;  // bf16 bytes per matrix
+// (fp32 [5][64]: cq, ck, b, ed, exp(gc_last)).  Each matrix is stored as the
+// MFMA A-operand images the state kernel loads, 1 KB each with lane l's 16
+// bytes at byte 16 l: image (w, kk) holds rows 16 w + l % 16, columns
+// 32 kk + 8 (l / 16) .. + 7, for wave w's rows.  The matrices are lower
+// triangular, so the zero upper-right 32 x 32 block has no image: waves 0
+// and 1 (rows 0..31) have only kk = 0, six images in all.  A lane-per-row
+// layout (each load instruction touching 16 rows, 64 bytes of each) made
+// the state kernel 15 us slower (262 -> 277 us at config 4 on MI355X): the
+// loads of adjacent lanes were not contiguous.
+constexpr int kMat = 6 * 512 * 2;  // bf16 bytes per matrix
 constexpr int kRec = 3 * kMat + 5 * kC * 4;    // 19712 = 77 * 256
 static_assert(kRec % 256 == 0, "records stay 256-byte aligned");
 
-// Element offset of (row, col) in a stored triangle (col < 32 for row < 32).
-__device__ __forceinline__ int tri_off(int row, int col) {
-  return row < 32 ? row * 32 + col : 1024 + (row - 32) * 64 + col;
-}
+// Image of operand kk of wave w (waves 0, 1: kk = 0 only; their kk = 1
+// maps to the kk = 0 image).
+__device__ __forceinline__ int img_index(int w, int kk) { return w < 2 ? w : 2 * w - 2 + kk; }
 // Padded rows of a sequence's last chunk store their (unused) outputs here,
 // so that every store in the chunk loop is unconditional: gfx9 counts loads
 // and stores in one in-order counter, and a store that only some paths
@@ -210,11 +215,13 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   __bf16* ail = reinterpret_cast<__bf16*>(rec + kMat);
   __bf16* aqp = reinterpret_cast<__bf16*>(rec + 2 * kMat);
   float* sc = reinterpret_cast<float*>(rec + 3 * kMat);
-  // Ai as hi and lo bf16 triangles.  Store j writes stored elements
-  // 512 j .. 512 j + 511, one contiguous KB (lane: 8 consecutive elements of
-  // one row), so every store instruction writes whole cache lines.
-  auto tri_row = [&](int j) { return j < 2 ? 16 * j + (lane >> 2) : 8 * j + 16 + (lane >> 3); };
-  auto tri_col = [&](int j) { return j < 2 ? (lane & 3) * 8 : (lane & 7) * 8; };
+  // Ai as hi and lo bf16 operand images.  Store j writes image j, one
+  // contiguous KB, so every store instruction writes whole cache lines;
+  // image j = img_index(w, kk) for (w, kk) = (0,0) (1,0) (2,0) (2,1) (3,0)
+  // (3,1).  Lane l reads X row 16 w + l % 16 from column 32 kk + 8 (l / 16):
+  // 8 lanes of one b128 read cover all 32 banks (row stride 68 = 4 mod 32).
+  auto tri_row = [&](int j) { return 16 * (j < 2 ? j : 2 + ((j - 2) >> 1)) + l15; };
+  auto tri_col = [&](int j) { return 32 * (j < 2 ? 0 : (j - 2) & 1) + 8 * lg; };
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
     bf8_t h, l;
@@ -353,12 +360,11 @@ __device__ __forceinline__ void load_inv(const ChunkParams& p, InvOps& ops, int6
   const __bf16* ail = reinterpret_cast<const __bf16*>(rec + kMat);
   const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
   // Rows 0..31 have no stored columns 32..63 (zero): their kk = 1 operand
-  // re-reads the kk = 0 one, keeping every load unconditional, and is never
-  // multiplied (the Vn product skips it).
+  // re-reads the kk = 0 image, keeping every load unconditional, and is
+  // never multiplied (the Vn product skips it).
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
-    const int row = wid * 16 + l15;
-    const int off = tri_off(row, (row < 32 ? 0 : kk * 32) + 8 * lg);
+    const int off = img_index(wid, kk) * 512 + 8 * lane;
     ops.aiH[kk] = *reinterpret_cast<const bf8_t*>(aih + off);
     ops.aiL[kk] = *reinterpret_cast<const bf8_t*>(ail + off);
   }
@@ -379,10 +385,8 @@ __device__ __forceinline__ void load_out(const ChunkParams& p, OutOps<K / 32>& o
   const __bf16* aqp = reinterpret_cast<const __bf16*>(rec + 2 * kMat);
   const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const int row = wid * 16 + l15;  // rows 0..31: kk = 1 as for Ai
-    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + tri_off(row, (row < 32 ? 0 : kk * 32) + 8 * lg));
-  }
+  for (int kk = 0; kk < 2; ++kk)  // waves 0, 1: kk = 1 as for Ai
+    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + img_index(wid, kk) * 512 + 8 * lane);
   ops.cq = sc[0 * kC + wid * 16 + l15];
 }
 
