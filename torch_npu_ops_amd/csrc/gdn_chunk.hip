@@ -306,7 +306,8 @@ struct __align__(16) P2Smem {
 // SIMD.
 template <int KK, int NV32>
 struct EarlyOps {
-  bf8_t kA[KK];          // K rows wid*16 + l15 (A operands)
+  bf8_t kA[KK];          // K rows wid*16.. as q4_load leaves them (q4_to_a makes them
+                         // A operands, rows wid*16 + l15, keys in q4_key order)
   bf8_t vA[NV32];        // v row wid*16 + l15, tile columns 32j + 8*lg .. + 7
                          // (A layout; select_op turns it into C layout)
   f4_t ck, bt;           // factors of rows wid*16 + 4*lg + i
@@ -318,7 +319,7 @@ struct InvOps {          // consumed by Vn = Ai R and ed * Vn
 };
 template <int KK>
 struct OutOps {          // consumed by the output o = cq (Q S) + Aq Vn
-  bf8_t qA[KK];          // Q rows wid*16 + l15
+  bf8_t qA[KK];          // Q rows wid*16.., as kA
   bf8_t aq[2];           // Aq rows wid*16 + l15
   float cq;              // factor of row wid*16 + l15
 };
@@ -336,10 +337,8 @@ __device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int l15 = lane & 15, lg = lane >> 4;
   const uint32_t rs = static_cast<uint32_t>(p.H) * K;
-  const bf16* kp = reinterpret_cast<const bf16*>(p.k) + tok_row(s, wid * 16 + l15, L) * rs +
-                   hq * K + 8 * lg;
-#pragma unroll
-  for (int kk = 0; kk < K / 32; ++kk) ops.kA[kk] = *reinterpret_cast<const bf8_t*>(kp + kk * 32);
+  const bf16* k0 = reinterpret_cast<const bf16*>(p.k) + hq * K;
+  q4_load([&](int r) { return k0 + tok_row(s, wid * 16 + r, L) * rs; }, ops.kA);
   const bf16* vp = reinterpret_cast<const bf16*>(p.v) + tok_row(s, wid * 16 + l15, L) * vrow +
                    vcol0 + 8 * lg;
 #pragma unroll
@@ -377,10 +376,8 @@ __device__ __forceinline__ void load_out(const ChunkParams& p, OutOps<K / 32>& o
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int l15 = lane & 15, lg = lane >> 4;
   const uint32_t rs = static_cast<uint32_t>(p.H) * K;
-  const bf16* qp = reinterpret_cast<const bf16*>(p.q) + tok_row(s, wid * 16 + l15, L) * rs +
-                   hq * K + 8 * lg;
-#pragma unroll
-  for (int kk = 0; kk < K / 32; ++kk) ops.qA[kk] = *reinterpret_cast<const bf8_t*>(qp + kk * 32);
+  const bf16* q0 = reinterpret_cast<const bf16*>(p.q) + hq * K;
+  q4_load([&](int r) { return q0 + tok_row(s, wid * 16 + r, L) * rs; }, ops.qA);
   const char* rec = rec_at(p, cidx, hv);
   const __bf16* aqp = reinterpret_cast<const __bf16*>(rec + 2 * kMat);
   const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
@@ -465,7 +462,8 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     load_inv(p, inv, cidx0, hv);
     __builtin_amdgcn_sched_barrier(0);
     load_out<K>(p, outo, bos, L0, cidx0, hv, hq);
-    store_kt<K, kLt>(sm.kt[0], opsA.kA, sel);
+    q4_to_a(opsA.kA);
+    store_kt_q4<kLt>(sm.kt[0], opsA.kA, sel);
   }
   __syncthreads();
 
@@ -482,7 +480,8 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     const int Ln = static_cast<int>(min<int64_t>(kC, eos - sn));
     load_early<K, BV>(p, nxt, sn, Ln, cidx0 + cn, hv, hq, vrow, vcol0);
 
-    // KS = K S (hi/lo S): rows wid*16.., columns nj*16..
+    // KS = K S (hi/lo S): rows wid*16.., columns nj*16..; S's keys are read
+    // in kA's order (q4_key).
     f4_t ks[NJ];
 #pragma unroll
     for (int nj = 0; nj < NJ; ++nj) ks[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
@@ -490,8 +489,8 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
       for (int nj = 0; nj < NJ; ++nj) {
-        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
-        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][q4_key(kk, lg)]);
+        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][q4_key(kk, lg)]);
         ks[nj] = mfma16(cur.kA[kk], sh, ks[nj]);
         ks[nj] = mfma16(cur.kA[kk], sl, ks[nj]);
       }
@@ -544,13 +543,14 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     // is the same sb read as S's B operand, and Q^T's B operand is Q's A
     // operand.  It must read sb before barrier 2: after it, a wave that is
     // ahead may already publish the next state into sb.
+    q4_to_a(outo.qA);
     f4_t qs[NJ];
 #pragma unroll
     for (int nj = 0; nj < NJ; ++nj) {
       qs[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
-        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][q4_key(kk, lg)]);
         qs[nj] = mfma16(sh, outo.qA[kk], qs[nj]);
       }
     }
@@ -607,7 +607,8 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       }
     }
     publish_state();
-    store_kt<K, kLt>(sm.kt[(ci + 1) & 1], nxt.kA, sel);
+    q4_to_a(nxt.kA);
+    store_kt_q4<kLt>(sm.kt[(ci + 1) & 1], nxt.kA, sel);
     __syncthreads();  // (3) state copy, next keys complete; vt / dt / kt reads done
   };
   // Unrolled by two so the operand buffers swap roles without copies.
