@@ -101,7 +101,7 @@ __device__ __forceinline__ char* rec_at(const ChunkParams& p, int64_t c, int hv)
   return p.rec + (c * p.HV + hv) * static_cast<int64_t>(kRec);
 }
 
-// Rows >= L of the K / Q operands (load_rows_op) repeat row L-1; here every
+// Rows >= L of the K / Q operands (q4_load) repeat row L-1; here every
 // consumer zeroes them through factors that are 0 there (beta, ck, ed, the
 // masks of M and Aq).
 
@@ -142,7 +142,9 @@ template <int K, typename GT, typename BT>
 __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   __shared__ __align__(16) float lds[4][kC][kLd];
   __shared__ float vec[4][4][kC];  // gc, beta, r_k, r_q per wave
-  const int wid = threadIdx.x >> 6;
+  // Wave index in a scalar register: the exit below is then a scalar branch,
+  // and the DPP transposes (q4_to_a) run with every lane of the wave active.
+  const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l15 = lane & 15, lg = lane >> 4;
   const int64_t c = blockIdx.x;
@@ -161,13 +163,17 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   constexpr int KK = K / 32;
   const int64_t rs = static_cast<int64_t>(p.H) * K;
 
-  // K rows of the chunk as MFMA operands (A and B^T read the same rows).
+  // K rows of the chunk as MFMA operands (A and B^T read the same rows),
+  // loaded quad-contiguously (q4_load; rows >= L repeat row L-1).  Every
+  // product here pairs two such operands, so q4_to_a's key order needs no
+  // change on the other side.
+  static_assert(K == 128, "q4 operand loads are 16 x 128");
+  const bf16* kbase = reinterpret_cast<const bf16*>(p.k) + static_cast<int64_t>(hq) * K;
+  const bf16* qbase = reinterpret_cast<const bf16*>(p.q) + static_cast<int64_t>(hq) * K;
   bf8_t kop[4][KK];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      kop[mi][kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
+    q4_load([&](int r) { return kbase + (s + min(mi * 16 + r, L - 1)) * rs; }, kop[mi]);
   // Per-token g (inclusive scan within the chunk) and beta; padded rows 0
   // (loads clamped to row L-1, then selected away).
   const int lt = min(lane, L - 1);
@@ -185,6 +191,8 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   // Row scales r = 1 / sqrt(sum x^2 + 1e-6) of the rows this lane holds
   // (row mi*16 + l15; the four lg lanes hold its four 32-wide pieces), or 1
   // without the in-op l2norm.
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) q4_to_a(kop[mi]);
   row_scales<KK>(kop, rkv, p.l2norm);
   __builtin_amdgcn_wave_barrier();
 
@@ -236,9 +244,9 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   bf8_t qop[4][KK];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
+    q4_load([&](int r) { return qbase + (s + min(mi * 16 + r, L - 1)) * rs; }, qop[mi]);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qop[mi][kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, rs, mi * 16, kk);
+  for (int mi = 0; mi < 4; ++mi) q4_to_a(qop[mi]);
   row_scales<KK>(qop, rqv, p.l2norm);
   __builtin_amdgcn_wave_barrier();
 
