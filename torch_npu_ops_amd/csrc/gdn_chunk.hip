@@ -566,8 +566,18 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 
     // o^T = cq (Q S)^T + Vn^T Aq^T (Vn^T's A operand is the vt read that
     // was Vn's B operand; Aq^T's B operand is Aq's A operand).
+    // The MFMA leaves lane (g = lane / 16, t = lane % 16) with row t,
+    // columns nj*16 + 4 g ..; before the store, lane (r = lane / 16, a =
+    // lane / 4 % 4, b = lane % 4) pulls (ds_bpermute) the values of row
+    // 4 a + r, column group b from lane 16 b + 4 a + r.  Each quad then
+    // writes 32 contiguous bytes of one row, where the MFMA layout had the 4
+    // lanes of a quad write 4 different rows (7 us of the state kernel at
+    // config 4 on MI355X).
+    static_assert(sizeof(T) == 2, "two dwords per 4-column group");
     {
-      const int row = wid * 16 + l15;
+      const int qa = (lane >> 2) & 3, qb = lane & 3, qr = lane >> 4;
+      const int src = 4 * (16 * qb + 4 * qa + qr);  // ds_bpermute byte address
+      const int row = wid * 16 + 4 * qa + qr;
       T* orow = row < L ? reinterpret_cast<T*>(p.o) + static_cast<uint64_t>(s + row) * vrow + vcol0
                         : reinterpret_cast<T*>(p.dump) + row * BV;
 #pragma unroll
@@ -584,7 +594,10 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
         Vec<T, 4> ov;
 #pragma unroll
         for (int i = 0; i < 4; ++i) ov.v[i] = from_f32<T>(acc[i]);
-        *reinterpret_cast<Vec<T, 4>*>(orow + nj * 16 + 4 * lg) = ov;
+        u32x2 w = __builtin_bit_cast(u32x2, ov);
+        w[0] = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(w[0]));
+        w[1] = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(w[1]));
+        *reinterpret_cast<u32x2*>(orow + nj * 16 + 4 * qb) = w;
       }
     }
     load_out<K>(p, outo, sn, Ln, cidx0 + cn, hv, hq);  // this chunk is done with `outo`
