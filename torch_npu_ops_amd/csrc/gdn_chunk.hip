@@ -334,23 +334,43 @@ struct OutOps {          // consumed by the output o = cq (Q S) + Aq Vn
 
 // Token row of q/k/v for C-layout row `r` (rows >= L read row L-1: finite,
 // and zeroed by their factors).
-__device__ __forceinline__ uint64_t tok_row(int64_t s, int r, int L) {
-  return static_cast<uint64_t>(s + min(r, L - 1));
+// The 16 rows of wave `wid` in a chunk starting at token s with L valid
+// rows: rows past L - 1 repeat row L - 1.  Split into a wave-uniform first
+// row (s + min(16 wid, L - 1)) and a per-lane row offset min(r, lw), lw =
+// L - 1 - min(16 wid, L - 1) >= 0, so every load address is a scalar base
+// plus a 32-bit lane offset (the saddr form of global loads): the 64-bit
+// per-lane address arithmetic this replaces was ~200 VALU instructions per
+// chunk step.
+struct WaveRows {
+  int64_t row0;  // first row (token index)
+  int lw;        // last valid row offset from row0
+};
+__device__ __forceinline__ WaveRows wave_rows(int64_t s, int L, int wid) {
+  const int f = min(16 * wid, L - 1);
+  return {s + f, L - 1 - f};
+}
+// Byte offset of element e of row offset r (clamped to lw) in rows of `rb` bytes.
+// (r <= 15 and rb < 2^24: a 24-bit multiply.)
+__device__ __forceinline__ uint32_t row_off(int r, int lw, uint32_t rb, int e) {
+  return __umul24(static_cast<uint32_t>(min(r, lw)), rb) + 2u * static_cast<uint32_t>(e);
 }
 
 template <int K, int BV>
 __device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32, BV / 32>& ops,
                                            int64_t s, int L, int64_t cidx, int hv, int hq,
                                            uint32_t vrow, int vcol0) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wid = wave_index();
   const int l15 = lane & 15, lg = lane >> 4;
   const uint32_t rs = static_cast<uint32_t>(p.H) * K;
-  const bf16* k0 = reinterpret_cast<const bf16*>(p.k) + hq * K;
-  q4_load([&](int r) { return k0 + tok_row(s, wid * 16 + r, L) * rs; }, ops.kA);
-  const bf16* vp = reinterpret_cast<const bf16*>(p.v) + tok_row(s, wid * 16 + l15, L) * vrow +
-                   vcol0 + 8 * lg;
+  const WaveRows wr = wave_rows(s, L, wid);
+  const char* kb = reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.k) +
+                                                 wr.row0 * rs + hq * K);
+  q4_load_b(kb, 2 * rs, wr.lw, ops.kA);
+  const char* vb = reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.v) +
+                                                 wr.row0 * vrow + vcol0);
 #pragma unroll
-  for (int j = 0; j < BV / 32; ++j) ops.vA[j] = *reinterpret_cast<const bf8_t*>(vp + 32 * j);
+  for (int j = 0; j < BV / 32; ++j)
+    ops.vA[j] = *reinterpret_cast<const bf8_t*>(vb + row_off(l15, wr.lw, 2 * vrow, 32 * j + 8 * lg));
   const float* sc = reinterpret_cast<const float*>(rec_at(p, cidx, hv) + 3 * kMat);
   const int r4 = wid * 16 + 4 * lg;
   ops.ck = *reinterpret_cast<const f4_t*>(sc + 1 * kC + r4);
@@ -360,20 +380,18 @@ __device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32
 
 __device__ __forceinline__ void load_inv(const ChunkParams& p, InvOps& ops, int64_t cidx,
                                          int hv) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int l15 = lane & 15, lg = lane >> 4;
+  const int lane = threadIdx.x & 63, wid = wave_index();
+  const int lg = lane >> 4;
   const char* rec = rec_at(p, cidx, hv);
-  const __bf16* aih = reinterpret_cast<const __bf16*>(rec);
-  const __bf16* ail = reinterpret_cast<const __bf16*>(rec + kMat);
   const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
   // Rows 0..31 have no stored columns 32..63 (zero): their kk = 1 operand
   // re-reads the kk = 0 image, keeping every load unconditional, and is
   // never multiplied (the Vn product skips it).
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
-    const int off = img_index(wid, kk) * 512 + 8 * lane;
-    ops.aiH[kk] = *reinterpret_cast<const bf8_t*>(aih + off);
-    ops.aiL[kk] = *reinterpret_cast<const bf8_t*>(ail + off);
+    const char* img = rec + img_index(wid, kk) * 1024;
+    ops.aiH[kk] = *reinterpret_cast<const bf8_t*>(img + 16 * lane);
+    ops.aiL[kk] = *reinterpret_cast<const bf8_t*>(img + kMat + 16 * lane);
   }
   ops.ed = *reinterpret_cast<const f4_t*>(sc + 3 * kC + wid * 16 + 4 * lg);
 }
@@ -381,17 +399,18 @@ __device__ __forceinline__ void load_inv(const ChunkParams& p, InvOps& ops, int6
 template <int K>
 __device__ __forceinline__ void load_out(const ChunkParams& p, OutOps<K / 32>& ops, int64_t s,
                                          int L, int64_t cidx, int hv, int hq) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int l15 = lane & 15, lg = lane >> 4;
+  const int lane = threadIdx.x & 63, wid = wave_index();
+  const int l15 = lane & 15;
   const uint32_t rs = static_cast<uint32_t>(p.H) * K;
-  const bf16* q0 = reinterpret_cast<const bf16*>(p.q) + hq * K;
-  q4_load([&](int r) { return q0 + tok_row(s, wid * 16 + r, L) * rs; }, ops.qA);
+  const WaveRows wr = wave_rows(s, L, wid);
+  const char* qb = reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.q) +
+                                                 wr.row0 * rs + hq * K);
+  q4_load_b(qb, 2 * rs, wr.lw, ops.qA);
   const char* rec = rec_at(p, cidx, hv);
-  const __bf16* aqp = reinterpret_cast<const __bf16*>(rec + 2 * kMat);
   const float* sc = reinterpret_cast<const float*>(rec + 3 * kMat);
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk)  // waves 0, 1: kk = 1 as for Ai
-    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(aqp + img_index(wid, kk) * 512 + 8 * lane);
+    ops.aq[kk] = *reinterpret_cast<const bf8_t*>(rec + 2 * kMat + img_index(wid, kk) * 1024 + 16 * lane);
   ops.cq = sc[0 * kC + wid * 16 + l15];
 }
 
@@ -403,7 +422,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   constexpr int KK = K / 32;
   constexpr int NJ = BV / 16;  // 16-column tiles per block
   const int tid = threadIdx.x;
-  const int wid = tid >> 6;
+  const int wid = wave_index();
   const int lane = tid & 63;
   const int l15 = lane & 15, lg = lane >> 4;
   // XCD-aware mapping: the nvt V tiles of one (sequence, head) get block ids
@@ -707,6 +726,9 @@ extern "C" int xk_gdn_chunk_fwd(
   if (beta_dtype != XK_F32 && beta_dtype != XK_BF16) return XK_ERR_UNSUPPORTED;
   if (cu_dtype != XK_I32 && cu_dtype != XK_I64) return XK_ERR_UNSUPPORTED;
   if (K != 128 || V % 32 != 0 || V <= 0) return XK_ERR_UNSUPPORTED;
+  // Row pitches of q / k and v / o in bytes feed 24-bit multiplies.
+  if (H * K * 2 >= (int64_t{1} << 24) || HV * V * 2 >= (int64_t{1} << 24))
+    return XK_ERR_UNSUPPORTED;
   if (N == 0 || total_tokens == 0) return XK_OK;
   // Token indices travel as int32 in the chunk table.
   if (total_tokens > INT32_MAX - kC) return XK_ERR_UNSUPPORTED;

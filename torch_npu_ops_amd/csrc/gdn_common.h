@@ -117,6 +117,24 @@ __device__ __forceinline__ void q4_load(RowPtr row, bf8_t (&r)[4]) {
   for (int h = 0; h < 4; ++h) r[h] = *reinterpret_cast<const bf8_t*>(row(4 * a + h) + 8 * chunk);
 }
 
+// q4_load with the rows given as a wave-uniform base, a row pitch of rb
+// bytes (< 2^24) and rows past lw clamped to lw: each address is the base
+// plus a 32-bit lane offset.
+__device__ __forceinline__ void q4_load_b(const char* base, uint32_t rb, int lw, bf8_t (&r)[4]) {
+  const int lane = threadIdx.x & 63;
+  const int a = (lane >> 2) & 3, chunk = 4 * (lane >> 4) + (lane & 3);
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const uint32_t off = __umul24(static_cast<uint32_t>(min(4 * a + h, lw)), rb) + 16u * chunk;
+    r[h] = *reinterpret_cast<const bf8_t*>(base + off);
+  }
+}
+
+// Wave index as a wave-uniform (scalar) value.
+__device__ __forceinline__ int wave_index() {
+  return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
 template <int CTRL>
 __device__ __forceinline__ bf8_t quad_dpp(const bf8_t& v) {
   typedef int i4_t __attribute__((ext_vector_type(4)));
