@@ -334,27 +334,6 @@ struct OutOps {          // consumed by the output o = cq (Q S) + Aq Vn
 
 // Token row of q/k/v for C-layout row `r` (rows >= L read row L-1: finite,
 // and zeroed by their factors).
-// The 16 rows of wave `wid` in a chunk starting at token s with L valid
-// rows: rows past L - 1 repeat row L - 1.  Split into a wave-uniform first
-// row (s + min(16 wid, L - 1)) and a per-lane row offset min(r, lw), lw =
-// L - 1 - min(16 wid, L - 1) >= 0, so every load address is a scalar base
-// plus a 32-bit lane offset (the saddr form of global loads): the 64-bit
-// per-lane address arithmetic this replaces was ~200 VALU instructions per
-// chunk step.
-struct WaveRows {
-  int64_t row0;  // first row (token index)
-  int lw;        // last valid row offset from row0
-};
-__device__ __forceinline__ WaveRows wave_rows(int64_t s, int L, int wid) {
-  const int f = min(16 * wid, L - 1);
-  return {s + f, L - 1 - f};
-}
-// Byte offset of element e of row offset r (clamped to lw) in rows of `rb` bytes.
-// (r <= 15 and rb < 2^24: a 24-bit multiply.)
-__device__ __forceinline__ uint32_t row_off(int r, int lw, uint32_t rb, int e) {
-  return __umul24(static_cast<uint32_t>(min(r, lw)), rb) + 2u * static_cast<uint32_t>(e);
-}
-
 template <int K, int BV>
 __device__ __forceinline__ void load_early(const ChunkParams& p, EarlyOps<K / 32, BV / 32>& ops,
                                            int64_t s, int L, int64_t cidx, int hv, int hq,
@@ -594,9 +573,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     // config 4 on MI355X).
     static_assert(sizeof(T) == 2, "two dwords per 4-column group");
     {
-      const int qa = (lane >> 2) & 3, qb = lane & 3, qr = lane >> 4;
-      const int src = 4 * (16 * qb + 4 * qa + qr);  // ds_bpermute byte address
-      const int row = wid * 16 + 4 * qa + qr;
+      const int row = wid * 16 + quad_row(), qb = quad_col();
       T* orow = row < L ? reinterpret_cast<T*>(p.o) + static_cast<uint64_t>(s + row) * vrow + vcol0
                         : reinterpret_cast<T*>(p.dump) + row * BV;
 #pragma unroll
@@ -613,10 +590,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
         Vec<T, 4> ov;
 #pragma unroll
         for (int i = 0; i < 4; ++i) ov.v[i] = from_f32<T>(acc[i]);
-        u32x2 w = __builtin_bit_cast(u32x2, ov);
-        w[0] = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(w[0]));
-        w[1] = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(w[1]));
-        *reinterpret_cast<u32x2*>(orow + nj * 16 + 4 * qb) = w;
+        *reinterpret_cast<u32x2*>(orow + nj * 16 + 4 * qb) = quad_rows(__builtin_bit_cast(u32x2, ov));
       }
     }
     load_out<K>(p, outo, sn, Ln, cidx0 + cn, hv, hq);  // this chunk is done with `outo`

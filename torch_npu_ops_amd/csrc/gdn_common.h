@@ -130,6 +130,47 @@ __device__ __forceinline__ void q4_load_b(const char* base, uint32_t rb, int lw,
   }
 }
 
+// The 16 rows of wave `wid` in a chunk starting at token s with L valid
+// rows: rows past L - 1 repeat row L - 1.  Split into a wave-uniform first
+// row (s + min(16 wid, L - 1)) and a per-lane row offset min(r, lw), lw =
+// L - 1 - min(16 wid, L - 1) >= 0, so every load address is a scalar base
+// plus a 32-bit lane offset (the saddr form of global loads): the 64-bit
+// per-lane address arithmetic this replaces was ~200 VALU instructions per
+// chunk step.
+struct WaveRows {
+  int64_t row0;  // first row (token index)
+  int lw;        // last valid row offset from row0
+};
+__device__ __forceinline__ WaveRows wave_rows(int64_t s, int L, int wid) {
+  const int f = min(16 * wid, L - 1);
+  return {s + f, L - 1 - f};
+}
+// Byte offset of element e of row offset r (clamped to lw) in rows of `rb` bytes.
+// (r <= 15 and rb < 2^24: a 24-bit multiply.)
+__device__ __forceinline__ uint32_t row_off(int r, int lw, uint32_t rb, int e) {
+  return __umul24(static_cast<uint32_t>(min(r, lw)), rb) + 2u * static_cast<uint32_t>(e);
+}
+
+// Quad-contiguous stores of MFMA-layout row pieces.  In the layouts that
+// give lane (g = lane / 16, t = lane % 16) row t, columns 4 g .. 4 g + 3 (8
+// bytes of bf16), the 4 lanes of a quad write 4 different rows.  quad_rows
+// hands lane (r = lane / 16, a = lane / 4 % 4, b = lane % 4) the piece of
+// row quad_row() = 4 a + r, column group quad_col() = b, read from lane
+// 16 b + 4 a + r (ds_bpermute), so each quad writes 32 contiguous bytes of
+// one row.  Every lane of the wave must be active.
+__device__ __forceinline__ int quad_row() {
+  const int lane = threadIdx.x & 63;
+  return 4 * ((lane >> 2) & 3) + (lane >> 4);
+}
+__device__ __forceinline__ int quad_col() { return threadIdx.x & 3; }
+__device__ __forceinline__ u32x2 quad_rows(u32x2 w) {
+  const int lane = threadIdx.x & 63;
+  const int src = 4 * (16 * (lane & 3) + 4 * ((lane >> 2) & 3) + (lane >> 4));  // byte address
+  w[0] = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(w[0]));
+  w[1] = __builtin_amdgcn_ds_bpermute(src, static_cast<int>(w[1]));
+  return w;
+}
+
 // Wave index as a wave-uniform (scalar) value.
 __device__ __forceinline__ int wave_index() {
   return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));

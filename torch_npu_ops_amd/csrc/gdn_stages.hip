@@ -398,8 +398,8 @@ struct __align__(16) FwdHSmem {
 // (select_op turns it into C layout) and, for lanes < 64, one token's gc.
 template <int KK>
 struct FwdHOps {
-  bf8_t ka[KK];
-  bf8_t wa[KK];
+  bf8_t ka[KK];  // K and w rows wid*16.. as q4_load_b leaves them; q4_to_a
+  bf8_t wa[KK];  // makes them A operands with keys in q4_key order
   bf8_t ua;
   float gct;
 };
@@ -408,7 +408,8 @@ template <int K>
 __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
   __shared__ FwdHSmem<K> sm;
   constexpr int KK = K / 32, M2 = K / 64;
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  static_assert(K == 128, "q4 operand loads are 16 x 128");
+  const int tid = threadIdx.x, wid = wave_index(), lane = tid & 63;
   const int l15 = lane & 15, lg = lane >> 4;
   const int64_t bid = blockIdx.x;
   const int64_t r = bid >> 3;
@@ -443,15 +444,18 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
 #pragma unroll
   for (int e = 0; e < 8; ++e)
     sel4[e] = static_cast<__bf16>(lg == (l15 >> 2) && e == (l15 & 3) ? 1.0f : 0.0f);
+  // K and w rows quad-contiguously (q4_load_b; the A-layout loads made each
+  // quad read 4 different rows).
   auto load_ops = [&](FwdHOps<KK>& o, int64_t ci) {
     const int64_t s = bos + ci * kC;
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      o.ka[kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, krow, wid * 16, kk);
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      o.wa[kk] = load_rows_op(p.w, static_cast<int64_t>(h) * K, s, L, wrow, wid * 16, kk);
+    const WaveRows wr = wave_rows(s, L, wid);
+    q4_load_b(reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.k) + wr.row0 * krow +
+                                            static_cast<int64_t>(hq) * K),
+              static_cast<uint32_t>(2 * krow), wr.lw, o.ka);
+    q4_load_b(reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.w) + wr.row0 * wrow +
+                                            static_cast<int64_t>(h) * K),
+              static_cast<uint32_t>(2 * wrow), wr.lw, o.wa);
     o.ua = *reinterpret_cast<const bf8_t*>(
         reinterpret_cast<const bf16*>(p.u) +
         ((s + min(wid * 16 + l15, L - 1)) * p.H + h) * static_cast<int64_t>(V) + v0 + 8 * lg);
@@ -460,7 +464,7 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
 
   // One chunk; `cur` holds its operands, `nxt` receives the next chunk's
   // (the last chunk loads itself again, so every load is unconditional).
-  auto step = [&](const FwdHOps<KK>& cur, FwdHOps<KK>& nxt, int64_t ci) {
+  auto step = [&](FwdHOps<KK>& cur, FwdHOps<KK>& nxt, int64_t ci) {
     const int64_t s = bos + ci * kC;
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
     const int64_t cidx = c0 + ci;
@@ -494,15 +498,21 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const f4_t t = mfma16(a, sel[hh], f4_t{0.f, 0.f, 0.f, 0.f});
-        const int r = l15 + 16 * hh, g = r >> 3, e = r & 7;
+        // Lane (lg, l15) now holds key row kappa(l15) and columns 4 lg ..;
+        // quad_rows regroups the lanes so each quad stores 32 contiguous
+        // bytes of one key row.
+        const int r = quad_row() + 16 * hh, g = r >> 3, e = r & 7;
         const int kr = wid * (K / 4) + (e < 4 ? 4 * g + e : 16 + 4 * g + e - 4);
         Vec<bf16, 4> o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o.v[i] = static_cast<bf16>(t[i]);
-        *reinterpret_cast<Vec<bf16, 4>*>(hdst + static_cast<int64_t>(kr) * V + v0 + nj * 16 + 4 * lg) = o;
+        *reinterpret_cast<u32x2*>(hdst + static_cast<int64_t>(kr) * V + v0 + nj * 16 + 4 * quad_col()) =
+            quad_rows(__builtin_bit_cast(u32x2, o));
       }
     }
-    store_kt<K, kLt>(sm.kt, cur.ka, sel);
+    q4_to_a(cur.ka);
+    store_kt_q4<kLt>(sm.kt, cur.ka, sel);
+    q4_to_a(cur.wa);
     if (tid < kC) sm.gc[tid] = cur.gct;
     __syncthreads();
     // WS = w S (hi / lo S) for rows wid*16.., then v_new = u - WS.
@@ -511,8 +521,8 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
     for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
       for (int nj = 0; nj < 2; ++nj) {
-        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
-        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][q4_key(kk, lg)]);
+        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][q4_key(kk, lg)]);
         ws[nj] = mfma16(cur.wa[kk], sh, ws[nj]);
         ws[nj] = mfma16(cur.wa[kk], sl, ws[nj]);
       }
@@ -537,13 +547,13 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
         // (their operands are clamped to it), so storing them at row L-1
         // rewrites the same values.
         const f4_t t = mfma16(vb, sel4, f4_t{0.f, 0.f, 0.f, 0.f});
-        const int row = wid * 16 + l15;
+        const int row = wid * 16 + quad_row();  // after quad_rows (quad-contiguous store)
         Vec<bf16, 4> o;
 #pragma unroll
         for (int i = 0; i < 4; ++i) o.v[i] = static_cast<bf16>(t[i]);
-        *reinterpret_cast<Vec<bf16, 4>*>(reinterpret_cast<bf16*>(p.vnew) +
-                                         ((s + min(row, L - 1)) * p.H + h) * static_cast<int64_t>(V) +
-                                         v0 + nj * 16 + 4 * lg) = o;
+        *reinterpret_cast<u32x2*>(reinterpret_cast<bf16*>(p.vnew) +
+                                  ((s + min(row, L - 1)) * p.H + h) * static_cast<int64_t>(V) +
+                                  v0 + nj * 16 + 4 * quad_col()) = quad_rows(__builtin_bit_cast(u32x2, o));
       }
       split4(d, dh, dl);
       *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][nj * 16 + l15][wid * 16 + 4 * lg]) = dh;
