@@ -30,12 +30,17 @@ namespace xk {
 namespace {
 
 constexpr int kThreads = 256;
+// The fused decode kernel keeps one block per (batch row, qk head) and
+// spreads each 64 KB state tile over 512 lanes (8 loads per lane): an
+// in-place stream of 64 KB tiles runs at 5.5 TB/s on MI355X with 16 loads
+// per lane, at 6.2 TB/s with 8.
+constexpr int kFusedThreads = 512;
 
 // Per-lane share of a K x V state tile.
-template <int K, int V>
+template <int K, int V, int NT = kThreads>
 struct Tile {
   static constexpr int kLanesPerRow = V / 4;               // float4 per lane
-  static constexpr int kRowsPerPass = kThreads / kLanesPerRow;
+  static constexpr int kRowsPerPass = NT / kLanesPerRow;
   static constexpr int kPasses = K / kRowsPerPass;
   static_assert(V % 4 == 0 && kLanesPerRow <= kWave && kWave % kLanesPerRow == 0,
                 "row of V must fit a wave");
@@ -45,12 +50,12 @@ struct Tile {
 
 // LDS shared by one block: normalised q/k (fp32), v, the reduction scratch
 // and the per-column results.
-template <int K, int V>
+template <int K, int V, int NT = kThreads>
 struct Smem {
   float q[K];
   float k[K];
   float v[V];
-  float red[2][kThreads / kWave][V];  // per-wave partials of h^T k, h^T q
+  float red[2][NT / kWave][V];  // per-wave partials of h^T k, h^T q
   float kh[V];
   float qh[V];
   float scal[4];  // k.q, ||q||^2, ||k||^2
@@ -130,10 +135,10 @@ __device__ __forceinline__ AB sigmoid_to(float x) {
 // One token of the recurrence on the register tile.  Inputs (q, k already
 // normalised and q scaled) are in sm.q / sm.k / sm.v.  Writes o[V] through
 // `out` (fp32 values, converted by the caller's store functor).
-template <int K, int V, typename StoreO>
-__device__ __forceinline__ void gdn_token(Tile<K, V>& t, Smem<K, V>& sm,
+template <int K, int V, int NT, typename StoreO>
+__device__ __forceinline__ void gdn_token(Tile<K, V, NT>& t, Smem<K, V, NT>& sm,
                                           float decay, float beta, StoreO store_o) {
-  using TL = Tile<K, V>;
+  using TL = Tile<K, V, NT>;
   const int tid = threadIdx.x;
   const int c4 = tid % TL::kLanesPerRow;  // column group (4 columns)
   const int r0 = tid / TL::kLanesPerRow;  // first row
@@ -171,7 +176,7 @@ __device__ __forceinline__ void gdn_token(Tile<K, V>& t, Smem<K, V>& sm,
   if (tid < V) {
     float a = 0.f, b = 0.f;
 #pragma unroll
-    for (int w = 0; w < kThreads / kWave; ++w) {
+    for (int w = 0; w < NT / kWave; ++w) {
       a += sm.red[0][w][tid];
       b += sm.red[1][w][tid];
     }
@@ -192,31 +197,33 @@ __device__ __forceinline__ void gdn_token(Tile<K, V>& t, Smem<K, V>& sm,
   }
 }
 
-template <int K, int V>
-__device__ __forceinline__ void load_tile(Tile<K, V>& t, const float* base) {
-  using TL = Tile<K, V>;
+template <int K, int V, int NT>
+// `pitch`: floats between rows in memory (the tile may be a column slice of
+// a wider state).
+__device__ __forceinline__ void load_tile(Tile<K, V, NT>& t, const float* base, int64_t pitch = V) {
+  using TL = Tile<K, V, NT>;
   const int c4 = threadIdx.x % TL::kLanesPerRow;
   const int r0 = threadIdx.x / TL::kLanesPerRow;
 #pragma unroll
   for (int i = 0; i < TL::kPasses; ++i) {
     const Vec<float, 4> v = ld_stream(reinterpret_cast<const Vec<float, 4>*>(
-        base + static_cast<int64_t>(r0 + i * TL::kRowsPerPass) * V + c4 * 4));
+        base + static_cast<int64_t>(r0 + i * TL::kRowsPerPass) * pitch + c4 * 4));
 #pragma unroll
     for (int c = 0; c < 4; ++c) t.h[i][c] = v.v[c];
   }
 }
 
-template <int K, int V>
-__device__ __forceinline__ void zero_tile(Tile<K, V>& t) {
+template <int K, int V, int NT>
+__device__ __forceinline__ void zero_tile(Tile<K, V, NT>& t) {
 #pragma unroll
-  for (int i = 0; i < Tile<K, V>::kPasses; ++i)
+  for (int i = 0; i < Tile<K, V, NT>::kPasses; ++i)
 #pragma unroll
     for (int c = 0; c < 4; ++c) t.h[i][c] = 0.f;
 }
 
-template <int K, int V>
-__device__ __forceinline__ void store_tile(const Tile<K, V>& t, float* base) {
-  using TL = Tile<K, V>;
+template <int K, int V, int NT>
+__device__ __forceinline__ void store_tile(const Tile<K, V, NT>& t, float* base, int64_t pitch = V) {
+  using TL = Tile<K, V, NT>;
   const int c4 = threadIdx.x % TL::kLanesPerRow;
   const int r0 = threadIdx.x / TL::kLanesPerRow;
 #pragma unroll
@@ -225,15 +232,15 @@ __device__ __forceinline__ void store_tile(const Tile<K, V>& t, float* base) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) v.v[c] = t.h[i][c];
     st_stream(reinterpret_cast<Vec<float, 4>*>(
-                  base + static_cast<int64_t>(r0 + i * TL::kRowsPerPass) * V + c4 * 4),
+                  base + static_cast<int64_t>(r0 + i * TL::kRowsPerPass) * pitch + c4 * 4),
               v);
   }
 }
 
 // Loads q and k of one token (raw), then l2-normalises (optional) and
 // scales q.  Block-wide; ends with a barrier.
-template <int K, int V, typename LoadQK>
-__device__ __forceinline__ void prep_qk(Smem<K, V>& sm, LoadQK load, bool l2norm,
+template <int K, int V, int NT, typename LoadQK>
+__device__ __forceinline__ void prep_qk(Smem<K, V, NT>& sm, LoadQK load, bool l2norm,
                                         float scale) {
   const int tid = threadIdx.x;
   // The previous token's readers of sm.q / sm.k / sm.scal are done.
@@ -303,11 +310,19 @@ struct RecParams {
   float sp_beta, sp_thr;
 };
 
-template <int K, int V, typename T, typename GT, typename BT>
+// NS blocks per (sequence, v head), each owning VT = V / NS state columns
+// (the recurrence is independent per column; q / k normalisation is
+// repeated per block).  At V = 128, NS = 2: an in-place stream of 64 KB
+// tiles with 16 loads per lane runs at 5.5 TB/s on MI355X, of 32 KB tiles
+// with 8 loads per lane at 6.3 TB/s.
+template <int K, int V, typename T, typename GT, typename BT, int NS>
 __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
-  __shared__ Smem<K, V> sm;
-  const int64_t n = blockIdx.x / p.HV;
-  const int hv = static_cast<int>(blockIdx.x % p.HV);
+  constexpr int VT = V / NS;
+  __shared__ Smem<K, VT> sm;
+  const int cs = static_cast<int>(blockIdx.x % NS);  // column slice
+  const int64_t item = blockIdx.x / NS;
+  const int64_t n = item / p.HV;
+  const int hv = static_cast<int>(item % p.HV);
   const int hq = hv / (p.HV / p.H);
   int64_t bos, len;
   if (p.cu) {
@@ -337,7 +352,7 @@ __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
     TokIn r;
     r.q = tid < K ? ldf<T>(p.q, (tok * p.H + hq) * K + tid) : 0.f;
     r.k = tid < K ? ldf<T>(p.k, (tok * p.H + hq) * K + tid) : 0.f;
-    r.v = tid < V ? ldf<T>(p.v, (tok * p.HV + hv) * V + tid) : 0.f;
+    r.v = tid < VT ? ldf<T>(p.v, (tok * p.HV + hv) * V + cs * VT + tid) : 0.f;
     r.g = ldf<GT>(p.g, tok * p.HV + hv);
     r.b = p.beta ? ldf<BT>(p.beta, tok * p.HV + hv) : 1.0f;
     if (p.gating) {
@@ -351,13 +366,14 @@ __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
   // complete in issue order, so the q/k normalisation then overlaps the
   // tile's latency instead of waiting behind it.
   TokIn cur = load_in(bos);
-  Tile<K, V> t;
+  Tile<K, VT> t;
   const int64_t s0 = slot_of(first_col);
   const bool s0_ok = p.h0 && s0 >= 0 && s0 < p.slots && first_col >= 0;
+  const int64_t col0 = static_cast<int64_t>(hv) * K * V + cs * VT;  // slice within a slot
   if (s0_ok)
-    load_tile<K, V>(t, p.h0 + s0 * p.h0_slot_stride + static_cast<int64_t>(hv) * K * V);
+    load_tile<K, VT>(t, p.h0 + s0 * p.h0_slot_stride + col0, V);
   else
-    zero_tile<K, V>(t);
+    zero_tile<K, VT>(t);
 
   // Per-token state writes: in place with a per-token slot column (2-D
   // indices or speculative decoding); otherwise once at the end.
@@ -366,37 +382,37 @@ __global__ void __launch_bounds__(kThreads) gdn_recurrent_kernel(RecParams p) {
     const int64_t tok = bos + i;
     // The next token's inputs are fetched while this one computes.
     const TokIn nxt = i + 1 < len ? load_in(tok + 1) : cur;
-    prep_qk<K, V>(sm, [&](int which, int) { return which == 0 ? cur.q : cur.k; },
-                  p.l2norm, p.scale);
-    if (tid < V) sm.v[tid] = cur.v;
+    prep_qk<K, VT>(sm, [&](int which, int) { return which == 0 ? cur.q : cur.k; },
+                   p.l2norm, p.scale);
+    if (tid < VT) sm.v[tid] = cur.v;
     const float decay = __expf(cur.g);
     const float beta = cur.b;
-    T* o = reinterpret_cast<T*>(p.o) + (tok * p.HV + hv) * V;
-    gdn_token<K, V>(t, sm, decay, beta, [&](int c, float val) { o[c] = from_f32<T>(val); });
+    T* o = reinterpret_cast<T*>(p.o) + (tok * p.HV + hv) * V + cs * VT;
+    gdn_token<K, VT>(t, sm, decay, beta, [&](int c, float val) { o[c] = from_f32<T>(val); });
     if (per_token) {
       const int64_t sl = slot_of(i);
-      if (sl >= 0 && sl < p.slots)
-        store_tile<K, V>(t, p.ht + sl * p.ht_slot_stride + static_cast<int64_t>(hv) * K * V);
+      if (sl >= 0 && sl < p.slots) store_tile<K, VT>(t, p.ht + sl * p.ht_slot_stride + col0, V);
     }
     cur = nxt;
   }
   if (!per_token) {
     if (p.inplace) {
       if (s0 >= 0 && s0 < p.slots && first_col >= 0)
-        store_tile<K, V>(t, p.ht + s0 * p.ht_slot_stride + static_cast<int64_t>(hv) * K * V);
+        store_tile<K, VT>(t, p.ht + s0 * p.ht_slot_stride + col0, V);
     } else {
-      store_tile<K, V>(t, p.ht + n * p.ht_slot_stride + static_cast<int64_t>(hv) * K * V);
+      store_tile<K, VT>(t, p.ht + n * p.ht_slot_stride + col0, V);
     }
   }
 }
 
 template <int K, int V, typename T, typename GT>
 int rec_beta(const RecParams& p, xk_dtype bdt, hipStream_t s) {
-  const dim3 grid(p.N * p.HV);
+  constexpr int NS = V == 128 ? 2 : 1;  // column slices per (sequence, head)
+  const dim3 grid(p.N * p.HV * NS);
   switch (bdt) {
-    case XK_F32: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, float>), grid, dim3(kThreads), 0, s, p); break;
-    case XK_BF16: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, bf16>), grid, dim3(kThreads), 0, s, p); break;
-    case XK_F16: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, f16>), grid, dim3(kThreads), 0, s, p); break;
+    case XK_F32: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, float, NS>), grid, dim3(kThreads), 0, s, p); break;
+    case XK_BF16: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, bf16, NS>), grid, dim3(kThreads), 0, s, p); break;
+    case XK_F16: hipLaunchKernelGGL((gdn_recurrent_kernel<K, V, T, GT, f16, NS>), grid, dim3(kThreads), 0, s, p); break;
     default: return XK_ERR_UNSUPPORTED;
   }
   return launch_status();
@@ -532,8 +548,9 @@ __device__ __forceinline__ void conv8(const FusedParams& p, int64_t b, int64_t c
 }
 
 template <int K, int V, typename T, typename GT, typename BT>
-__global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p) {
-  __shared__ Smem<K, V> sm;
+__global__ void __launch_bounds__(kFusedThreads) gdn_conv_decode_kernel(FusedParams p) {
+  constexpr int NT = kFusedThreads;
+  __shared__ Smem<K, V, NT> sm;
   __shared__ float xv_lds[K * 2];          // q and k after conv + SiLU
   __shared__ float vv_lds[16][V];          // v heads of the group (R <= 16)
   const int64_t b = blockIdx.x / p.H;
@@ -550,7 +567,7 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
   const bool st_ok = sslot >= 0 && sslot < p.slots;
   // The first v head's state tile is requested before the conv phase, so
   // its 64 KB stream overlaps the conv loads and arithmetic.
-  Tile<K, V> t;
+  Tile<K, V, NT> t;
   {
     float* sbase = p.state + sslot * p.st_slot_stride + static_cast<int64_t>(h) * R * K * V;
     if (st_ok) load_tile<K, V>(t, sbase); else zero_tile<K, V>(t);
@@ -568,7 +585,7 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
   if (p.conv_vec) {
     // 8 channels per lane (K and V are multiples of 8, so a group never
     // straddles the q / k / v parts).
-    for (int i = tid * 8; i < nch; i += kThreads * 8) {
+    for (int i = tid * 8; i < nch; i += NT * 8) {
       float y[8];
       switch (p.S) {
         case 1: conv8<T, 1>(p, b, cslot, conv_ok, chan(i), y); break;
@@ -580,7 +597,7 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
       for (int c = 0; c < 8; ++c) put(i + c, y[c]);
     }
   } else {
-  for (int i = tid; i < nch; i += kThreads) {
+  for (int i = tid; i < nch; i += NT) {
     int64_t ch;
     if (i < K) ch = static_cast<int64_t>(h) * K + i;
     else if (i < 2 * K) ch = static_cast<int64_t>(p.H) * K + static_cast<int64_t>(h) * K + (i - K);
@@ -608,8 +625,8 @@ __global__ void __launch_bounds__(kThreads) gdn_conv_decode_kernel(FusedParams p
   // while head j computes (two register tiles, unrolled by two): 204.4 ->
   // 197.8 us at config 5 on MI355X, the state stream no longer pausing
   // between the group's heads.
-  Tile<K, V> t2;
-  auto head = [&](Tile<K, V>& cur, Tile<K, V>& nxt, int j) {
+  Tile<K, V, NT> t2;
+  auto head = [&](Tile<K, V, NT>& cur, Tile<K, V, NT>& nxt, int j) {
     const int hv = h * R + j;
     float* sbase = p.state + sslot * p.st_slot_stride + static_cast<int64_t>(hv) * K * V;
     if (j + 1 < R) {
@@ -639,9 +656,9 @@ template <int K, int V, typename T, typename GT>
 int fused_beta(const FusedParams& p, xk_dtype bdt, hipStream_t s) {
   const dim3 grid(p.B * p.H);
   switch (bdt) {
-    case XK_F32: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, float>), grid, dim3(kThreads), 0, s, p); break;
-    case XK_BF16: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, bf16>), grid, dim3(kThreads), 0, s, p); break;
-    case XK_F16: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, f16>), grid, dim3(kThreads), 0, s, p); break;
+    case XK_F32: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, float>), grid, dim3(kFusedThreads), 0, s, p); break;
+    case XK_BF16: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, bf16>), grid, dim3(kFusedThreads), 0, s, p); break;
+    case XK_F16: hipLaunchKernelGGL((gdn_conv_decode_kernel<K, V, T, GT, f16>), grid, dim3(kFusedThreads), 0, s, p); break;
     default: return XK_ERR_UNSUPPORTED;
   }
   return launch_status();
