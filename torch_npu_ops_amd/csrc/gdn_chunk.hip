@@ -216,6 +216,15 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
     }
   __builtin_amdgcn_wave_barrier();
 
+  // Q rows, loaded before the inverse so that their latency hides behind
+  // it (252 VGPRs with them live; the LDS footprint already limits the
+  // kernel to two waves per SIMD, so the registers cost no occupancy).
+  // Measured on MI355X at config 4: 87.6 -> 84.4 us.
+  bf8_t qop[4][KK];
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+    q4_load([&](int r) { return qbase + (s + min(mi * 16 + r, L - 1)) * rs; }, qop[mi]);
+
   invert_unit_lower(X);  // X = (I + M)^-1, row-major
 
   char* rec = rec_at(p, c, hv);
@@ -239,12 +248,6 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   }
   __builtin_amdgcn_wave_barrier();
 
-  // Q rows, loaded only now so that they are not live (64 registers)
-  // through the inverse.
-  bf8_t qop[4][KK];
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
-    q4_load([&](int r) { return qbase + (s + min(mi * 16 + r, L - 1)) * rs; }, qop[mi]);
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) q4_to_a(qop[mi]);
   row_scales<KK>(qop, rqv, p.l2norm);
