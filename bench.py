@@ -250,6 +250,8 @@ class RopeInplaceCase(Case):
     T, H, HID, RD = 16384, 16, 512, 64
     # rope part of x read + written, sin / cos read (bf16)
     algo_bytes = T * H * RD * 2 * 2 + 2 * T * RD * 2
+    # (rows, row bytes, rotated tail bytes) for the strided-pattern floor
+    tail_floor = (T * H, HID * 2, RD * 2)
 
     def __init__(self):
         g = torch.Generator().manual_seed(0)
@@ -1022,6 +1024,9 @@ def measure_lib():
         lib.xkm_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
                                  ctypes.c_void_p]
         lib.xkm_copy.restype = ctypes.c_int
+        lib.xkm_tail_rw.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
+                                    ctypes.c_int64, ctypes.c_void_p]
+        lib.xkm_tail_rw.restype = ctypes.c_int
         _MEASURE = lib
     return _MEASURE
 
@@ -1049,6 +1054,33 @@ class CopyFloorCase(Case):
             def run(src=src, dst=dst):
                 _ok(lib.xkm_copy(src.data_ptr(), dst.data_ptr(), self.nbytes, _cur_stream()),
                     lib)
+            out.append(run)
+        return out
+
+
+class TailFloorCase(Case):
+    """In-place read-modify-write of the last `tail` bytes of `rows` rows of
+    `pitch` bytes, one 16-byte vector per lane and nothing else: the floor
+    of an op whose HBM traffic has that strided pattern (rope_inplace),
+    timed in the same harness."""
+    timing = "graph"
+    kernel = "tail_rw_kernel"
+
+    def __init__(self, rows, pitch, tail):
+        self.rows, self.pitch, self.tail = rows, pitch, tail
+        self.algo_bytes = 2 * rows * tail
+        self.name = f"tail_rw_{rows}x{tail}of{pitch}"
+        self.config = f"in-place rewrite of the last {tail} B of {rows} rows of {pitch} B"
+
+    def sets(self, dev, n):
+        lib = measure_lib()
+        out = []
+        for _ in range(n):
+            x = torch.zeros(self.rows * self.pitch, dtype=torch.uint8, device=dev)
+
+            def run(x=x):
+                _ok(lib.xkm_tail_rw(x.data_ptr(), self.rows, self.pitch, self.tail,
+                                    _cur_stream()), lib)
             out.append(run)
         return out
 
@@ -1457,6 +1489,13 @@ def main():
                            False) * 1e3
             ops[name]["same_traffic_copy_us"] = round(cus, 2)
             ops[name]["vs_copy"] = round(ms * 1e3 / cus, 3)
+        tail = getattr(case, "tail_floor", None)
+        if tail:
+            # The op's strided access pattern alone, without its loads of
+            # other operands or its arithmetic.
+            tus = time_gpu(TailFloorCase(*tail), dev, args.steps, args.warmup, False) * 1e3
+            ops[name]["strided_tail_floor_us"] = round(tus, 2)
+            ops[name]["vs_strided_tail_floor"] = round(ms * 1e3 / tus, 3)
         print(f"[bench] {name}: {ms*1e3:.2f} us/call, {gbs:.0f} GB/s "
               f"({gbs / HBM_PEAK_GBS:.1%} of peak)"
               + (f", {ops[name]['tokens/s']:.3g} tokens/s, "

@@ -1,6 +1,7 @@
 // Reference kernels for bench.py's floors: an empty kernel (the launch
-// floor) and a plain device copy (the floor of an HBM-bound kernel that
-// moves the same bytes).  Measurement only: built into libxk_measure.so,
+// floor), a plain device copy (the floor of an HBM-bound kernel that
+// moves the same bytes) and an in-place read-modify-write of the last
+// bytes of every row (the floor of a kernel with that strided pattern).  Measurement only: built into libxk_measure.so,
 // loaded by bench.py, and not part of the C-ABI in include/xk_ops.h.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -17,6 +18,16 @@ __global__ void __launch_bounds__(256) copy16_kernel(const u32x4* __restrict__ s
                                                      u32x4* __restrict__ dst, int64_t n16) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < n16) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+// The last `tail` bytes of each of `rows` rows of `pitch` bytes, read and
+// written back changed, one 16-byte vector per lane (lpr lanes per row).
+__global__ void __launch_bounds__(256) tail_rw_kernel(char* x, int64_t rows, int64_t pitch,
+                                                      int64_t tail, int lpr) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= rows * lpr) return;
+  u32x4* p = reinterpret_cast<u32x4*>(x + (i / lpr) * pitch + (pitch - tail) + 16 * (i % lpr));
+  *p = *p ^ 1u;
 }
 
 }  // namespace
@@ -37,5 +48,20 @@ extern "C" int xkm_copy(const void* src, void* dst, int64_t bytes, void* stream)
   hipLaunchKernelGGL(copy16_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
                      static_cast<u32x4*>(dst), n16);
+  return static_cast<int>(hipGetLastError());
+}
+
+// Strided in-place floor: rows x tail bytes at the end of rows of `pitch`
+// bytes (tail and pitch multiples of 16, tail <= pitch, x 16-byte aligned);
+// reads and writes rows * tail bytes.
+extern "C" int xkm_tail_rw(void* x, int64_t rows, int64_t pitch, int64_t tail, void* stream) {
+  if (rows <= 0 || tail <= 0 || tail > pitch || tail % 16 != 0 || pitch % 16 != 0) return -1;
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0 || tail / 16 > 1024) return -1;
+  const int lpr = static_cast<int>(tail / 16);
+  const int64_t blocks = (rows * lpr + 255) / 256;
+  if (blocks > INT32_MAX) return -1;
+  hipLaunchKernelGGL(tail_rw_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<char*>(x), rows, pitch, tail,
+                     lpr);
   return static_cast<int>(hipGetLastError());
 }
