@@ -303,7 +303,7 @@ constexpr int kLt = kC + 8;  // bf16 LDS row stride (144 B: 16-byte aligned)
 template <int K, int BV>
 struct __align__(16) P2Smem {
   __bf16 sb[2][BV][K + 8];    // state hi / lo, transposed: sb[h][v][k]
-  __bf16 kt[2][K][kLt];       // chunk keys transposed, double-buffered
+  __bf16 kr[2][kC * K];       // chunk key rows (kr_off layout), double-buffered
   __bf16 rt[2][BV][kLt];      // R transposed, hi / lo
   __bf16 vt[BV][kLt];         // Vn transposed (bf16, for the output)
   __bf16 dt[2][BV][kLt];      // (ed * Vn) transposed, hi / lo
@@ -317,8 +317,8 @@ struct __align__(16) P2Smem {
 // SIMD.
 template <int KK, int NV32>
 struct EarlyOps {
-  bf8_t kA[KK];          // K rows wid*16.. as q4_load leaves them (q4_to_a makes them
-                         // A operands, rows wid*16 + l15, keys in q4_key order)
+  bf8_t kA[KK];          // K rows wid*16.. as q4_load leaves them (stored as they are
+                         // into the chunk's key tile, store_kr_q4)
   bf8_t vA[NV32];        // v row wid*16 + l15, tile columns 32j + 8*lg .. + 7
                          // (A layout; select_op turns it into C layout)
   f4_t ck, bt;           // factors of rows wid*16 + 4*lg + i
@@ -471,8 +471,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     load_inv(p, inv, cidx0, hv);
     __builtin_amdgcn_sched_barrier(0);
     load_out<K>(p, outo, bos, L0, cidx0, hv, hq);
-    q4_to_a(opsA.kA);
-    store_kt_q4<kLt>(sm.kt[0], opsA.kA, sel);
+    store_kr_q4(sm.kr[0], opsA.kA, wid);
   }
   __syncthreads();
 
@@ -489,20 +488,23 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
     const int Ln = static_cast<int>(min<int64_t>(kC, eos - sn));
     load_early<K, BV>(p, nxt, sn, Ln, cidx0 + cn, hv, hq, vrow, vcol0);
 
-    // KS = K S (hi/lo S): rows wid*16.., columns nj*16..; S's keys are read
-    // in kA's order (q4_key).
+    // KS = K S (hi/lo S): rows wid*16.., columns nj*16..; K's rows come
+    // from the chunk's key tile.
+    const __bf16* kr = sm.kr[ci & 1];
     f4_t ks[NJ];
 #pragma unroll
     for (int nj = 0; nj < NJ; ++nj) ks[nj] = f4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
+    for (int kk = 0; kk < KK; ++kk) {
+      const bf8_t ka = kr_a(kr, wid, kk);
 #pragma unroll
       for (int nj = 0; nj < NJ; ++nj) {
-        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][q4_key(kk, lg)]);
-        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][q4_key(kk, lg)]);
-        ks[nj] = mfma16(cur.kA[kk], sh, ks[nj]);
-        ks[nj] = mfma16(cur.kA[kk], sl, ks[nj]);
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+        ks[nj] = mfma16(ka, sh, ks[nj]);
+        ks[nj] = mfma16(ka, sl, ks[nj]);
       }
+    }
     // R = b v - ck KS  ->  rt (transposed, hi / lo); padded rows are 0.
 #pragma unroll
     for (int nj = 0; nj < NJ; ++nj) {
@@ -600,14 +602,12 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 
     // S <- exp(gc_last) S + K^T (ed Vn) on the wave's register rows, then
     // its bf16 copy (every wave finished reading sb before barrier 2).
-    const __bf16 (*kt)[kLt] = sm.kt[ci & 1];
 #pragma unroll
     for (int m2 = 0; m2 < M2; ++m2) {
       const int mi = wid * M2 + m2;
       bf8_t ka[2];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        ka[kk] = *reinterpret_cast<const bf8_t*>(&kt[mi * 16 + l15][kk * 32 + 8 * lg]);
+      for (int kk = 0; kk < 2; ++kk) ka[kk] = kr_at(kr, mi, kk);
 #pragma unroll
       for (int nj = 0; nj < NJ; ++nj) {
         f4_t acc = sreg[m2][nj];
@@ -624,9 +624,8 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
       }
     }
     publish_state();
-    q4_to_a(nxt.kA);
-    store_kt_q4<kLt>(sm.kt[(ci + 1) & 1], nxt.kA, sel);
-    __syncthreads();  // (3) state copy, next keys complete; vt / dt / kt reads done
+    store_kr_q4(sm.kr[(ci + 1) & 1], nxt.kA, wid);
+    __syncthreads();  // (3) state copy, next keys complete; vt / dt / key reads done
   };
   // Unrolled by two so the operand buffers swap roles without copies.
   for (int64_t ci = 0; ci < nch; ci += 2) {

@@ -212,6 +212,60 @@ __device__ __forceinline__ void q4_to_a(bf8_t (&r)[4]) {
 // Key offset of slot g (lane / 16) of operand kk in q4_to_a's order.
 __device__ __forceinline__ constexpr int q4_key(int kk, int g) { return 32 * g + 8 * kk; }
 
+// ---------------------------------------------------------------------------
+// A chunk's 64 x 128 bf16 key rows kept row-major in LDS and read both as
+// rows (A operands of K S) and as columns (A operands of K^T X).  Rows are
+// 256 bytes, unpadded; 16-byte chunk c of row r sits at chunk c ^ (r & 15),
+// which keeps the raw quad-contiguous stores (store_kr_q4) and the row reads
+// (kr_a) free of bank conflicts.
+//
+// Column reads use gfx950's ds_read_b64_tr_b16.  In each group of 16 lanes,
+// element i (of 4) of lane j is element j % 4 of the 8 bytes that lane
+// 4 i + j / 4 addressed (checked on MI355X with an index-valued tile).  So
+// when lane s addresses row r0 + s / 4, columns c0 + 4 (s % 4) .. + 3, lane
+// j receives column c0 + j at rows r0 .. r0 + 3: four consecutive k of an
+// MFMA operand whose rows are the tile's columns.
+// ---------------------------------------------------------------------------
+constexpr int kKrRow = 128;  // bf16 per key row
+__device__ __forceinline__ int kr_off(int r, int chunk) {
+  return r * kKrRow + ((chunk ^ (r & 15)) << 3);
+}
+
+// The raw q4_load pieces of rows wid*16 .. wid*16 + 15 (load h: lane
+// 16 g + 4 a + b holds row 4 a + h, chunk 4 g + b) into the tile.
+__device__ __forceinline__ void store_kr_q4(__bf16* kr, const bf8_t (&r)[4], int wid) {
+  const int lane = threadIdx.x & 63;
+  const int a = (lane >> 2) & 3, chunk = 4 * (lane >> 4) + (lane & 3);
+#pragma unroll
+  for (int h = 0; h < 4; ++h)
+    *reinterpret_cast<bf8_t*>(kr + kr_off(wid * 16 + 4 * a + h, chunk)) = r[h];
+}
+
+// A operand kk of rows wid*16 ..: lane row wid*16 + lane % 16, keys
+// 32 kk + 8 (lane / 16) .. + 7.
+__device__ __forceinline__ bf8_t kr_a(const __bf16* kr, int wid, int kk) {
+  const int lane = threadIdx.x & 63;
+  return *reinterpret_cast<const bf8_t*>(kr + kr_off(wid * 16 + (lane & 15), 4 * kk + (lane >> 4)));
+}
+
+// A operand of the transpose: lane key 16 mi + lane % 16, rows (tokens)
+// 32 kk + 8 (lane / 16) .. + 7, as two transposed 4-row reads.
+__device__ __forceinline__ bf8_t kr_at(const __bf16* kr, int mi, int kk) {
+  typedef short s4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s4_t lds_s4;
+  const int lane = threadIdx.x & 63;
+  const int s = lane & 15, g = lane >> 4;
+  const int col = 16 * mi + 4 * (s & 3);
+  s4_t v[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int r = 32 * kk + 8 * g + 4 * h + (s >> 2);
+    const __bf16* p = kr + kr_off(r, col >> 3) + (col & 7);
+    v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p));
+  }
+  return __builtin_bit_cast(bf8_t, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 // store_kt for A operands in q4_to_a's key order (K = 128).
 template <int LD>
 __device__ __forceinline__ void store_kt_q4(__bf16 (*kt)[LD], const bf8_t (&kA)[4],
