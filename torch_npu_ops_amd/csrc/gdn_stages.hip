@@ -388,7 +388,7 @@ struct FwdHParams : Seq {
 template <int K>
 struct __align__(16) FwdHSmem {
   __bf16 sb[2][kBV][K + 8];  // state hi / lo, transposed: sb[h][v][k]
-  __bf16 kt[K][kLt];         // chunk keys transposed
+  __bf16 kr[kC * K];         // chunk key rows (kr_off layout)
   __bf16 dt[2][kBV][kLt];    // decayed v_new transposed, hi / lo
   float gc[kC];
 };
@@ -398,8 +398,9 @@ struct __align__(16) FwdHSmem {
 // (select_op turns it into C layout) and, for lanes < 64, one token's gc.
 template <int KK>
 struct FwdHOps {
-  bf8_t ka[KK];  // K and w rows wid*16.. as q4_load_b leaves them; q4_to_a
-  bf8_t wa[KK];  // makes them A operands with keys in q4_key order
+  bf8_t ka[KK];  // K and w rows wid*16.. as q4_load_b leaves them: K is stored
+  bf8_t wa[KK];  // as it is into the key tile, q4_to_a makes w A operands with
+                 // keys in q4_key order
   bf8_t ua;
   float gct;
 };
@@ -510,8 +511,7 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
             quad_rows(__builtin_bit_cast(u32x2, o));
       }
     }
-    q4_to_a(cur.ka);
-    store_kt_q4<kLt>(sm.kt, cur.ka, sel);
+    store_kr_q4(sm.kr, cur.ka, wid);
     q4_to_a(cur.wa);
     if (tid < kC) sm.gc[tid] = cur.gct;
     __syncthreads();
@@ -567,8 +567,7 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
       const int mi = wid * M2 + m2;
       bf8_t kA[2];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        kA[kk] = *reinterpret_cast<const bf8_t*>(&sm.kt[mi * 16 + l15][kk * 32 + 8 * lg]);
+      for (int kk = 0; kk < 2; ++kk) kA[kk] = kr_at(sm.kr, mi, kk);
 #pragma unroll
       for (int nj = 0; nj < 2; ++nj) {
         f4_t acc = sreg[m2][nj];
@@ -584,7 +583,7 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
         sreg[m2][nj] = acc;
       }
     }
-    __syncthreads();  // sb / kt / dt / gc are rewritten by the next chunk
+    __syncthreads();  // sb / kr / dt / gc are rewritten by the next chunk
   };
   FwdHOps<KK> opsA, opsB;
   if (nch > 0) load_ops(opsA, 0);
