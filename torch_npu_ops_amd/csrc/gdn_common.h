@@ -248,22 +248,25 @@ __device__ __forceinline__ bf8_t kr_a(const __bf16* kr, int wid, int kk) {
   return *reinterpret_cast<const bf8_t*>(kr + kr_off(wid * 16 + (lane & 15), 4 * kk + (lane >> 4)));
 }
 
-// A operand of the transpose: lane key 16 mi + lane % 16, rows (tokens)
-// 32 kk + 8 (lane / 16) .. + 7, as two transposed 4-row reads.
-__device__ __forceinline__ bf8_t kr_at(const __bf16* kr, int mi, int kk) {
-  typedef short s4_t __attribute__((ext_vector_type(4)));
+// Column 16 mi + lane % 16 of the tile at rows r0 .. r0 + 3 (r0 may differ
+// between the 16-lane groups, not within one), as 4 bf16 bit patterns.
+typedef short s4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s4_t kr_col4(const __bf16* kr, int mi, int r0) {
   typedef __attribute__((address_space(3))) s4_t lds_s4;
-  const int lane = threadIdx.x & 63;
-  const int s = lane & 15, g = lane >> 4;
+  const int s = threadIdx.x & 15;
   const int col = 16 * mi + 4 * (s & 3);
-  s4_t v[2];
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int r = 32 * kk + 8 * g + 4 * h + (s >> 2);
-    const __bf16* p = kr + kr_off(r, col >> 3) + (col & 7);
-    v[h] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p));
-  }
-  return __builtin_bit_cast(bf8_t, __builtin_shufflevector(v[0], v[1], 0, 1, 2, 3, 4, 5, 6, 7));
+  const __bf16* p = kr + kr_off(r0 + (s >> 2), col >> 3) + (col & 7);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p));
+}
+__device__ __forceinline__ bf8_t cat_bf8(s4_t a, s4_t b) {
+  return __builtin_bit_cast(bf8_t, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// A operand of the transpose: lane column (key) 16 mi + lane % 16, rows
+// (tokens) 32 kk + 8 (lane / 16) .. + 7, as two transposed 4-row reads.
+__device__ __forceinline__ bf8_t kr_at(const __bf16* kr, int mi, int kk) {
+  const int r0 = 32 * kk + 8 * ((threadIdx.x & 63) >> 4);
+  return cat_bf8(kr_col4(kr, mi, r0), kr_col4(kr, mi, r0 + 4));
 }
 
 // store_kt for A operands in q4_to_a's key order (K = 128).

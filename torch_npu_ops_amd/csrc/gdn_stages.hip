@@ -624,8 +624,8 @@ struct FwdOParams : Seq {
 
 template <int K, int V>
 struct __align__(16) FwdOSmem {
-  __bf16 ht[V][K + 8];   // h_c transposed: ht[v][k]
-  __bf16 vt[V][kLt];     // v_new transposed: vt[v][token]; rows >= L zero
+  __bf16 hr[K * V];   // h_c rows hr[k][v] (kr_off layout)
+  __bf16 vr[kC * V];  // v_new rows vr[token][v] (kr_off layout); rows >= L zero
   float gc[kC];
 };
 
@@ -633,13 +633,14 @@ struct __align__(16) FwdOSmem {
 // 16w .. 16w + 15.  Everything is computed transposed, o^T = h^T q^T +
 // v^T Aq^T, so that a lane owns one token and 4 consecutive columns of it
 // (one 8-byte store per 16 columns):
-//  * h and v_new reach LDS transposed through select_op MFMAs (exact), as
-//    8-byte vectors;
+//  * h and v_new are loaded as whole rows and stored in LDS as they are;
+//    their transposes are read with ds_read_b64_tr_b16 (kr_col4);
 //  * Aq^T = (k q^T masked and decayed, rounded to bf16 as the reference's
 //    A.to(v), chunk_o.py:113) stays in registers: its MFMA C layout holds 4
 //    consecutive key tokens per lane, and two such tiles form the B operand
 //    with the key tokens in the order {4g .. 4g+3, 16+4g .. 16+4g+3}; the
-//    matching A operand reads the same tokens of vt as two 8-byte halves.
+//    matching A operand reads the same tokens of v_new as two transposed
+//    4-row reads.
 template <int K, int V>
 __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
   static_assert(K == 128 && V == 128, "head dims of 128");
@@ -653,55 +654,33 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
   int L;
   if (!locate_chunk(p, c, n, s, L) || c >= p.hcap) return;  // block-uniform
   const int hq = h / (p.H / p.Hg);
-  const bf8_t sel[2] = {select_op(0), select_op(1)};
   const f4_t zero = {0.f, 0.f, 0.f, 0.f};
 
-  // Every global operand is loaded before its first use: h and v_new rows
-  // for the transposes, then q and the key tiles of Aq, which stay in flight
-  // across the barrier.
-  // h_c rows 32w .. 32w + 31 -> ht (transposed).
+  // Every global operand is loaded before its first use: h and v_new rows,
+  // then q and the key tiles of Aq, which stay in flight across the
+  // barrier.  Each 16 lanes load one whole 256-byte row.
+  static_assert(V == kKrRow, "row tiles of 128 bf16");
+  const int rl = lane >> 4, ch = lane & 15;  // row within a load, 16-byte chunk
   const bf16* hsrc = reinterpret_cast<const bf16*>(p.h) + (c * p.H + h) * static_cast<int64_t>(K) * V;
-  bf8_t ha[2][V / 32];
+  bf8_t hv[8];  // h_c rows 32w + 4j + rl
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int j = 0; j < 8; ++j)
+    hv[j] = *reinterpret_cast<const bf8_t*>(hsrc + (wid * 32 + 4 * j + rl) * V + 8 * ch);
+  bf8_t vv[4];  // v_new rows (tokens) 16w + 4j + rl
 #pragma unroll
-    for (int kk = 0; kk < V / 32; ++kk)
-      ha[mt][kk] = *reinterpret_cast<const bf8_t*>(hsrc + (wid * 32 + mt * 16 + l15) * V + kk * 32 + 8 * lg);
-  const int t = wid * 16 + l15;
-  const bf16* vsrc = reinterpret_cast<const bf16*>(p.v) +
-                     ((s + min(t, L - 1)) * p.H + h) * static_cast<int64_t>(V);
-  bf8_t va[V / 32];
-#pragma unroll
-  for (int kk = 0; kk < V / 32; ++kk) va[kk] = *reinterpret_cast<const bf8_t*>(vsrc + kk * 32 + 8 * lg);
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int k0 = wid * 32 + mt * 16;
-#pragma unroll
-    for (int kk = 0; kk < V / 32; ++kk)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const f4_t tt = mfma16(ha[mt][kk], sel[hh], zero);
-        Vec<__bf16, 4> b;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(tt[i]);
-        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.ht[kk * 32 + hh * 16 + l15][k0 + 4 * lg]) = b;
-      }
+  for (int j = 0; j < 4; ++j) {
+    const int t = wid * 16 + 4 * j + rl;
+    vv[j] = *reinterpret_cast<const bf8_t*>(reinterpret_cast<const bf16*>(p.v) +
+                                            ((s + min(t, L - 1)) * p.H + h) * static_cast<int64_t>(V) +
+                                            8 * ch);
   }
-  // v_new rows (tokens) 16w .. 16w + 15 -> vt (transposed), rows >= L zero.
-  {
-    bf8_t a[V / 32];
 #pragma unroll
-    for (int kk = 0; kk < V / 32; ++kk) a[kk] = t < L ? va[kk] : bf8_t{};
+  for (int j = 0; j < 8; ++j)
+    *reinterpret_cast<bf8_t*>(sm.hr + kr_off(wid * 32 + 4 * j + rl, ch)) = hv[j];
 #pragma unroll
-    for (int kk = 0; kk < V / 32; ++kk)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const f4_t r = mfma16(a[kk], sel[hh], zero);
-        Vec<__bf16, 4> b;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(r[i]);
-        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.vt[kk * 32 + hh * 16 + l15][wid * 16 + 4 * lg]) = b;
-      }
+  for (int j = 0; j < 4; ++j) {
+    const int t = wid * 16 + 4 * j + rl;
+    *reinterpret_cast<bf8_t*>(sm.vr + kr_off(t, ch)) = t < L ? vv[j] : bf8_t{};
   }
   if (tid < kC) sm.gc[tid] = p.gcum ? p.gcum[(s + min(tid, L - 1)) * p.H + h] : 0.f;
   const int64_t qrow = static_cast<int64_t>(p.Hg) * K;
@@ -751,22 +730,14 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
   for (int nj = 0; nj < NJ; ++nj) {
     f4_t acc = zero;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      acc = mfma16(*reinterpret_cast<const bf8_t*>(&sm.ht[nj * 16 + l15][kk * 32 + 8 * lg]),
-                   qa[kk], acc);
+    for (int kk = 0; kk < KK; ++kk) acc = mfma16(kr_at(sm.hr, nj, kk), qa[kk], acc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] *= eg;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       if (m * 32 > wid * 16 + 15) continue;  // key tokens beyond the diagonal
-      const Vec<__bf16, 4> lo = *reinterpret_cast<const Vec<__bf16, 4>*>(&sm.vt[nj * 16 + l15][m * 32 + 4 * lg]);
-      const Vec<__bf16, 4> hi = *reinterpret_cast<const Vec<__bf16, 4>*>(&sm.vt[nj * 16 + l15][m * 32 + 16 + 4 * lg]);
-      bf8_t va;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        va[i] = lo.v[i];
-        va[4 + i] = hi.v[i];
-      }
+      const bf8_t va = cat_bf8(kr_col4(sm.vr, nj, m * 32 + 4 * lg),
+                               kr_col4(sm.vr, nj, m * 32 + 16 + 4 * lg));
       acc = mfma16(va, aqb[m], acc);
     }
     if (tq < L) {
