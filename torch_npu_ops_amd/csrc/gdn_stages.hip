@@ -273,7 +273,7 @@ constexpr int kLt = kC + 8;  // bf16 LDS row stride (144 B: 16-byte aligned)
 template <typename BT, typename AT>
 __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
   constexpr int D = 128;  // K = V = 128
-  __shared__ __align__(16) __bf16 bt[2][D][kLt];  // rhs^T hi / lo: bt[.][d][token]
+  __shared__ __align__(16) __bf16 bt[2][kC * D];  // rhs rows hi / lo (kr_off layout)
   __shared__ float fb[kC], fk[kC];
   const int h = blockIdx.y;
   int64_t n, s;
@@ -304,39 +304,40 @@ __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
       }
     }
   }
-  const bf8_t sel[2] = {select_op(0), select_op(1)};
   const f4_t zero = {0.f, 0.f, 0.f, 0.f};
+  static_assert(D == kKrRow, "row tiles of 128 bf16");
+  const int rl = lane >> 4, ch = lane & 15;  // row within a load, 16-byte chunk
   __syncthreads();  // fb / fk
 
 #pragma unroll 1
   for (int prod = 0; prod < 2; ++prod) {
     // prod 0: u = Ai (v beta); prod 1: w = Ai (k beta exp(gc)).
-    const bf16* src = prod == 0
-        ? reinterpret_cast<const bf16*>(p.v) + ((s + min(tq, L - 1)) * p.H + h) * D
-        : reinterpret_cast<const bf16*>(p.k) + ((s + min(tq, L - 1)) * p.Hg + hq) * D;
+    // Right-hand-side rows (tokens) 16w + 4j + rl, each loaded whole by 16
+    // lanes, scaled by the token's factor (0 for rows >= L, whose loads
+    // repeat row L-1) and split hi / lo into the row tiles.
     const float* f = prod == 0 ? fb : fk;
-    bf8_t a[D / 32];
+    bf8_t a[4];
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk) {
-      a[kk] = *reinterpret_cast<const bf8_t*>(src + kk * 32 + 8 * lg);
-      if (tq >= L) a[kk] = bf8_t{};
+    for (int j = 0; j < 4; ++j) {
+      const int64_t t = s + min(wid * 16 + 4 * j + rl, L - 1);
+      const bf16* src = prod == 0 ? reinterpret_cast<const bf16*>(p.v) + (t * p.H + h) * D
+                                  : reinterpret_cast<const bf16*>(p.k) + (t * p.Hg + hq) * D;
+      a[j] = *reinterpret_cast<const bf8_t*>(src + 8 * ch);
     }
-    f4_t fr;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fr[i] = f[wid * 16 + 4 * lg + i];
+    for (int j = 0; j < 4; ++j) {
+      const int t = wid * 16 + 4 * j + rl;
+      const float fr = t < L ? f[t] : 0.f;
+      bf8_t xh, xl;
 #pragma unroll
-    for (int kk = 0; kk < D / 32; ++kk)
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        f4_t x = mfma16(a[kk], sel[hh], zero);  // tokens 16w + 4lg + i, column 32kk + 16hh + l15
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] *= fr[i];
-        Vec<__bf16, 4> xh, xl;
-        split4(x, xh, xl);
-        const int d = kk * 32 + hh * 16 + l15;
-        *reinterpret_cast<Vec<__bf16, 4>*>(&bt[0][d][wid * 16 + 4 * lg]) = xh;
-        *reinterpret_cast<Vec<__bf16, 4>*>(&bt[1][d][wid * 16 + 4 * lg]) = xl;
+      for (int e = 0; e < 8; ++e) {
+        const float x = fr * static_cast<float>(a[j][e]);
+        xh[e] = static_cast<__bf16>(x);
+        xl[e] = static_cast<__bf16>(x - static_cast<float>(xh[e]));
       }
+      *reinterpret_cast<bf8_t*>(bt[0] + kr_off(t, ch)) = xh;
+      *reinterpret_cast<bf8_t*>(bt[1] + kr_off(t, ch)) = xl;
+    }
     __syncthreads();  // bt complete
 
     bf16* orow = reinterpret_cast<bf16*>(prod == 0 ? p.u : p.w) +
@@ -347,8 +348,8 @@ __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         if (kk * 32 > wid * 16 + 15) continue;  // key tokens beyond the diagonal
-        const bf8_t bh = *reinterpret_cast<const bf8_t*>(&bt[0][nj * 16 + l15][kk * 32 + 8 * lg]);
-        const bf8_t bl = *reinterpret_cast<const bf8_t*>(&bt[1][nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t bh = kr_at(bt[0], nj, kk);  // rhs^T: column nj*16 + l15, tokens 32kk + 8lg ..
+        const bf8_t bl = kr_at(bt[1], nj, kk);
         acc = mfma16(bh, aih[kk], acc);
         acc = mfma16(bl, aih[kk], acc);
         if constexpr (std::is_same<AT, float>::value) acc = mfma16(bh, ail[kk], acc);
