@@ -141,7 +141,9 @@ struct KktParams : Seq {
 template <int K, typename BT>
 __global__ void __launch_bounds__(kTh) chunk_kkt_kernel(KktParams p) {
   __shared__ float vec[4][2][kC];  // gc, beta per wave
-  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // Wave index in a scalar register: the exit below is a scalar branch, and
+  // the DPP transposes (q4_to_a) run with every lane of the wave active.
+  const int wid = wave_index(), lane = threadIdx.x & 63;
   const int l15 = lane & 15, lg = lane >> 4;
   const int h = blockIdx.y * 4 + wid;
   int64_t n, s;
@@ -149,13 +151,18 @@ __global__ void __launch_bounds__(kTh) chunk_kkt_kernel(KktParams p) {
   if (!(h < p.H && locate_chunk(p, blockIdx.x, n, s, L))) return;  // wave-uniform
   const int hq = h / (p.H / p.Hg);
   constexpr int KK = K / 32;
+  // Key rows loaded quad-contiguously (q4_load; rows >= L repeat row L-1)
+  // and made A operands in registers; both operands of K K^T carry the same
+  // key order, so the products are unchanged.
+  static_assert(K == 128, "q4 operand loads are 16 x 128");
+  const bf16* kbase = reinterpret_cast<const bf16*>(p.k) + static_cast<int64_t>(hq) * K;
+  const int64_t rs = static_cast<int64_t>(p.Hg) * K;
   bf8_t kop[4][KK];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
+    q4_load([&](int r) { return kbase + (s + min(mi * 16 + r, L - 1)) * rs; }, kop[mi]);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      kop[mi][kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L,
-                                 static_cast<int64_t>(p.Hg) * K, mi * 16, kk);
+  for (int mi = 0; mi < 4; ++mi) q4_to_a(kop[mi]);
   const int lt = min(lane, L - 1);
   vec[wid][0][lane] = p.gcum ? p.gcum[(s + lt) * p.H + h] : 0.f;
   vec[wid][1][lane] = ldf<BT>(p.beta, (s + lt) * p.H + h);
