@@ -269,6 +269,13 @@ __device__ __forceinline__ bf8_t kr_at(const __bf16* kr, int mi, int kk) {
   return cat_bf8(kr_col4(kr, mi, r0), kr_col4(kr, mi, r0 + 4));
 }
 
+// kr_at with the rows in q4_to_a's key order: rows q4_key(kk, lane / 16)
+// .. + 7, the partner of an operand kk that went through q4_to_a.
+__device__ __forceinline__ bf8_t kr_at_q4(const __bf16* kr, int mi, int kk) {
+  const int r0 = 32 * ((threadIdx.x & 63) >> 4) + 8 * kk;
+  return cat_bf8(kr_col4(kr, mi, r0), kr_col4(kr, mi, r0 + 4));
+}
+
 // store_kt for A operands in q4_to_a's key order (K = 128).
 template <int LD>
 __device__ __forceinline__ void store_kt_q4(__bf16 (*kt)[LD], const bf8_t (&kA)[4],

@@ -649,8 +649,12 @@ struct __align__(16) FwdOSmem {
 //    with the key tokens in the order {4g .. 4g+3, 16+4g .. 16+4g+3}; the
 //    matching A operand reads the same tokens of v_new as two transposed
 //    4-row reads.
+// Three waves per SIMD (the LDS allows three blocks per CU) need at most
+// 168 VGPRs: 166 with the cap against 172 without it, and the uncapped
+// kernel (two waves per SIMD) took 205 us at config 4 on MI355X against 173.
 template <int K, int V>
-__global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
+__global__ void __launch_bounds__(kTh) __attribute__((amdgpu_waves_per_eu(3)))
+chunk_fwd_o_kernel(FwdOParams p) {
   static_assert(K == 128 && V == 128, "head dims of 128");
   __shared__ FwdOSmem<K, V> sm;
   constexpr int KK = K / 32, NJ = V / 16;
@@ -693,16 +697,21 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
   if (tid < kC) sm.gc[tid] = p.gcum ? p.gcum[(s + min(tid, L - 1)) * p.H + h] : 0.f;
   const int64_t qrow = static_cast<int64_t>(p.Hg) * K;
   const int tq = wid * 16 + l15;  // this lane's output token
+  // q rows and the key rows of Aq, loaded quad-contiguously (q4_load; rows
+  // >= L repeat row L-1) and made A operands in registers with the keys in
+  // q4_key order, which every product below matches on its other side.
+  static_assert(K == 128, "q4 operand loads are 16 x 128");
+  const bf16* qbase = reinterpret_cast<const bf16*>(p.q) + static_cast<int64_t>(hq) * K;
+  const bf16* kbase = reinterpret_cast<const bf16*>(p.k) + static_cast<int64_t>(hq) * K;
   bf8_t qa[KK], ka[4][KK];
-#pragma unroll
-  for (int kk = 0; kk < KK; ++kk)
-    qa[kk] = load_rows_op(p.q, static_cast<int64_t>(hq) * K, s, L, qrow, wid * 16, kk);
+  q4_load([&](int r) { return qbase + (s + min(wid * 16 + r, L - 1)) * qrow; }, qa);
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      ka[j][kk] = load_rows_op(p.k, static_cast<int64_t>(hq) * K, s, L, qrow, j * 16, kk);
+    q4_load([&](int r) { return kbase + (s + min(j * 16 + r, L - 1)) * qrow; }, ka[j]);
   __syncthreads();
+  q4_to_a(qa);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) q4_to_a(ka[j]);
 
   const float gq = sm.gc[tq];
 
@@ -738,7 +747,7 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_o_kernel(FwdOParams p) {
   for (int nj = 0; nj < NJ; ++nj) {
     f4_t acc = zero;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) acc = mfma16(kr_at(sm.hr, nj, kk), qa[kk], acc);
+    for (int kk = 0; kk < KK; ++kk) acc = mfma16(kr_at_q4(sm.hr, nj, kk), qa[kk], acc);
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] *= eg;
 #pragma unroll
