@@ -197,23 +197,27 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   __builtin_amdgcn_wave_barrier();
 
   // M = strict_tril(b_i r_i r_j (k_i . k_j) exp(gc_i - gc_j)) into X (the
-  // ten lower 16x16 tiles; the strictly upper ones are never read).
+  // ten lower 16x16 tiles; the strictly upper ones are never read).  The
+  // product K_nj K_mi^T is tile (mi, nj) transposed, so a lane holds row
+  // mi*16 + l15, columns nj*16 + 4 lg .. + 3, written as one 16-byte vector.
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < 4; ++mi) {
+    const int row = mi * 16 + l15;
+    const float fr = btv[row] * rkv[row], gr = gcv[row];
 #pragma unroll
     for (int nj = 0; nj <= mi; ++nj) {
       f4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) a = mfma16(kop[mi][kk], kop[nj][kk], a);
+      for (int kk = 0; kk < KK; ++kk) a = mfma16(kop[nj][kk], kop[mi][kk], a);
+      f4_t m;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = mi * 16 + 4 * lg + i, col = nj * 16 + l15;
-        float m = 0.f;
-        if (row > col)
-          m = btv[row] * rkv[row] * rkv[col] * a[i] * __expf(gcv[row] - gcv[col]);
-        X[row][col] = m;
+        const int col = nj * 16 + 4 * lg + i;
+        m[i] = row > col ? fr * rkv[col] * a[i] * __expf(gr - gcv[col]) : 0.f;
       }
+      *reinterpret_cast<f4_t*>(&X[row][nj * 16 + 4 * lg]) = m;
     }
+  }
   __builtin_amdgcn_wave_barrier();
 
   // Q rows, loaded before the inverse so that their latency hides behind
@@ -253,25 +257,29 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   row_scales<KK>(qop, rqv, p.l2norm);
   __builtin_amdgcn_wave_barrier();
 
-  // Aq = scale * tril(r_q r_k (q k^T) exp(gc_i - gc_j)), rows < L.
+  // Aq = scale * tril(r_q r_k (q k^T) exp(gc_i - gc_j)), rows < L, formed
+  // transposed like M (K_nj Q_mi^T) for 16-byte row writes.
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < 4; ++mi) {
+    const int row = mi * 16 + l15;
+    const float fr = p.scale * rqv[row], gr = gcv[row];
 #pragma unroll
     for (int nj = 0; nj < 4; ++nj) {
       f4_t a = {0.f, 0.f, 0.f, 0.f};
       if (nj <= mi) {
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) a = mfma16(qop[mi][kk], kop[nj][kk], a);
+        for (int kk = 0; kk < KK; ++kk) a = mfma16(kop[nj][kk], qop[mi][kk], a);
       }
+      f4_t val;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int row = mi * 16 + 4 * lg + i, col = nj * 16 + l15;
-        float val = 0.f;
-        if (nj <= mi && row >= col && row < L)
-          val = p.scale * rqv[row] * rkv[col] * a[i] * __expf(gcv[row] - gcv[col]);
-        X[row][col] = val;
+        const int col = nj * 16 + 4 * lg + i;
+        val[i] = nj <= mi && row >= col && row < L ? fr * rkv[col] * a[i] * __expf(gr - gcv[col])
+                                                    : 0.f;
       }
+      *reinterpret_cast<f4_t*>(&X[row][nj * 16 + 4 * lg]) = val;
     }
+  }
   __builtin_amdgcn_wave_barrier();
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
