@@ -478,43 +478,102 @@ __device__ __forceinline__ bf8_t load_rows_op(const void* base, int64_t col_off,
   return *reinterpret_cast<const bf8_t*>(src);
 }
 
+// 16x16x16 bf16 MFMA: lane l holds A[l%16][4(l/16)+e], B[4(l/16)+e][l%16]
+// and C[4(l/16)+i][l%16], so a C fragment is already a B operand.
+__device__ __forceinline__ f4_t mfma16k16(s4_t a, s4_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ void split4s(const f4_t& x, s4_t& h, s4_t& l) {
+  Vec<__bf16, 4> hh, ll;
+  split4(x, hh, ll);
+  h = __builtin_bit_cast(s4_t, hh);
+  l = __builtin_bit_cast(s4_t, ll);
+}
+// hi/lo-split product (hi*hi + hi*lo + lo*hi) on 16x16x16 tiles.
+__device__ __forceinline__ f4_t mfma16k16_split3(s4_t ah, s4_t al, s4_t bh, s4_t bl, f4_t c) {
+  c = mfma16k16(ah, bh, c);
+  c = mfma16k16(ah, bl, c);
+  return mfma16k16(al, bh, c);
+}
+
 // ---------------------------------------------------------------------------
 // X <- (I + M)^-1 for a strictly lower M in the wave's LDS tile X (only the
 // strictly lower entries of the ten lower 16x16 tiles are read); the result
 // is written back row-major (fp32, zeros above the diagonal).  One wave.
-//   * the two 32x32 diagonal blocks by forward substitution, lane (b, cc)
-//     forming column cc of X_bb: x[i] = delta_{i,cc} - sum_{j<i} M[i][j] x[j];
-//   * the off-diagonal block X_10 = -X_11 (M_10 X_00) with hi/lo-split MFMAs.
-// This is the 16->64 block merge of solve_tril.py:266-320 with 32-wide
-// diagonal blocks.
+//   * the four 16x16 diagonal blocks by forward substitution, lane (g, c)
+//     forming column c of X_gg: x[i] = delta_{i,c} - sum_{j<i} M[i][j] x[j];
+//   * each pair of them merged into a 32x32 block, X_10 = -X_11 (M_10 X_00)
+//     on 16x16x16 hi/lo-split MFMAs;
+//   * the two 32x32 blocks merged the same way on 16x16x32 MFMAs.
+// This is the 16->64 block merge of solve_tril.py:266-320.  Against 32x32
+// diagonal blocks by substitution (a 32-deep chain of up to 31 FMAs per
+// lane, 496 per lane in all; 120 now), measured on MI355X at config 4: the
+// chunked prep kernel 83.1 -> 76.1 us, solve_tril 49.1 -> 40.8 us.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void invert_unit_lower(float (*X)[kLd]) {
   const int lane = threadIdx.x & 63;
   const int l15 = lane & 15, lg = lane >> 4;
-  const int b = lane >> 5, cc = lane & 31, base = b * 32;
-  float x[32];
+  const int b = lane >> 5, cc = lane & 31;
+  const f4_t zero = {0.f, 0.f, 0.f, 0.f};
+  {
+    // Diagonal blocks: group lg takes X_gg, g = lg.
+    float x[16];
+    const int o = 16 * lg;
 #pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const float* mr = &X[base + i][base];
-    float a0 = (i == cc) ? 1.f : 0.f, a1 = 0.f;
+    for (int i = 0; i < 16; ++i) {
+      const float* mr = &X[o + i][o];
+      float a0 = (i == l15) ? 1.f : 0.f, a1 = 0.f;
 #pragma unroll
-    for (int j = 0; j + 1 < i; j += 2) {
-      a0 = fmaf(-mr[j], x[j], a0);
-      a1 = fmaf(-mr[j + 1], x[j + 1], a1);
+      for (int j = 0; j + 1 < i; j += 2) {
+        a0 = fmaf(-mr[j], x[j], a0);
+        a1 = fmaf(-mr[j + 1], x[j + 1], a1);
+      }
+      if (i & 1) a0 = fmaf(-mr[i - 1], x[i - 1], a0);
+      x[i] = a0 + a1;
     }
-    if (i & 1) a0 = fmaf(-mr[i - 1], x[i - 1], a0);
-    x[i] = a0 + a1;
+    __builtin_amdgcn_wave_barrier();
+    // Each group stores its block once transposed (a row of X_gg^T per
+    // lane, 16-byte writes) and once row-major (a column per lane), at
+    // disjoint places in spent diagonal blocks and the unused upper part:
+    //   g = 0: X_0^T at [0,16)x[0,16)   (B operand below; part of X_00^T)
+    //   g = 1: X_1^T at [16,32)x[16,32) (part of X_00^T), X_1 at [0,16)x[16,32)
+    //   g = 2: X_2^T at [32,48)x[48,64) (B operand),      X_2 at [32,48)x[32,48)
+    //   g = 3:                                            X_3 at [48,64)x[48,64)
+    // and the unneeded two to [0,16)x[32,64), which the 64-merge rewrites.
+    const int tr = (lg == 1 ? 16 : lg == 2 ? 32 : 0) + l15;
+    const int tc = lg == 0 ? 0 : lg == 1 ? 16 : lg == 2 ? 48 : 32;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      *reinterpret_cast<f4_t*>(&X[tr][tc + 4 * t]) = f4_t{x[4 * t], x[4 * t + 1], x[4 * t + 2], x[4 * t + 3]};
+    const int cr = lg == 2 ? 32 : lg == 3 ? 48 : 0;
+    const int ccol = (lg == 0 ? 48 : lg == 1 ? 16 : lg == 2 ? 32 : 48) + l15;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) X[cr + i][ccol] = x[i];
   }
   __builtin_amdgcn_wave_barrier();
-  // X_00 transposed into the (spent) M_00 block, X_11 row-major into M_11.
-  if (b == 0) {
+  // 16 -> 32: pair p (rows 32p ..): T = M' X_even, C = X_odd T, with M' =
+  // M[32p+16 ..][32p ..], X_even from its transpose, X_odd row-major.
+  f4_t cp[2];
 #pragma unroll
-    for (int i = 0; i < 32; i += 4)
-      *reinterpret_cast<f4_t*>(&X[cc][i]) = f4_t{x[i], x[i + 1], x[i + 2], x[i + 3]};
-  } else {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) X[32 + i][32 + cc] = x[i];
+  for (int p = 0; p < 2; ++p) {
+    const int o = 32 * p;
+    s4_t a1h, a1l, b1h, b1l, a2h, a2l, th, tl;
+    split4s(*reinterpret_cast<const f4_t*>(&X[o + 16 + l15][o + 4 * lg]), a1h, a1l);
+    split4s(*reinterpret_cast<const f4_t*>(&X[o + l15][o + 16 * p + 4 * lg]), b1h, b1l);
+    const f4_t t = mfma16k16_split3(a1h, a1l, b1h, b1l, zero);
+    split4s(t, th, tl);
+    split4s(*reinterpret_cast<const f4_t*>(&X[p ? 48 + l15 : l15][16 + 32 * p + 4 * lg]), a2h, a2l);
+    cp[p] = mfma16k16_split3(a2h, a2l, th, tl, zero);
   }
+  __builtin_amdgcn_wave_barrier();
+  // X_00 transposed into [0,32)^2: -C_0 transposed (16-byte writes) and the
+  // zero block; X_11 row-major into [32,64)^2: -C_0's partner -C_1 and the
+  // zero block.  Lane (lg, l15) holds C[4 lg + i][l15].
+  *reinterpret_cast<f4_t*>(&X[l15][16 + 4 * lg]) = -cp[0];
+  *reinterpret_cast<f4_t*>(&X[16 + l15][4 * lg]) = zero;
+  *reinterpret_cast<f4_t*>(&X[32 + l15][48 + 4 * lg]) = zero;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) X[48 + 4 * lg + i][32 + l15] = -cp[1][i];
   __builtin_amdgcn_wave_barrier();
 
   // T = M_10 X_00 (32 x 32).
@@ -552,6 +611,18 @@ __device__ __forceinline__ void invert_unit_lower(float (*X)[kLd]) {
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
         x10[mt][nt] = mfma_split3(ah, al, bh[nt], bl[nt], f4_t{0.f, 0.f, 0.f, 0.f});
+    }
+  }
+  // Column cc of X_00 (lanes 0..31), read back from its transpose.
+  float x[32];
+  if (b == 0) {
+#pragma unroll
+    for (int i = 0; i < 32; i += 4) {
+      const f4_t v = *reinterpret_cast<const f4_t*>(&X[cc][i]);
+      x[i] = v[0];
+      x[i + 1] = v[1];
+      x[i + 2] = v[2];
+      x[i + 3] = v[3];
     }
   }
   __builtin_amdgcn_wave_barrier();
