@@ -276,46 +276,6 @@ __device__ __forceinline__ bf8_t kr_at_q4(const __bf16* kr, int mi, int kk) {
   return cat_bf8(kr_col4(kr, mi, r0), kr_col4(kr, mi, r0 + 4));
 }
 
-// store_kt for A operands in q4_to_a's key order (K = 128).
-template <int LD>
-__device__ __forceinline__ void store_kt_q4(__bf16 (*kt)[LD], const bf8_t (&kA)[4],
-                                            const bf8_t (&sel)[2]) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int l15 = lane & 15, lg = lane >> 4;
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const f4_t c = mfma16(kA[kk], sel[h], f4_t{0.f, 0.f, 0.f, 0.f});
-      Vec<__bf16, 4> b;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(c[i]);
-      // slot 16 h + l15 = 8 (2 h + l15 / 8) + l15 % 8
-      const int key = q4_key(kk, 2 * h + (l15 >> 3)) + (l15 & 7);
-      *reinterpret_cast<Vec<__bf16, 4>*>(&kt[key][wid * 16 + 4 * lg]) = b;
-    }
-}
-
-// Keys of the lane's A operands (rows wave*16 + lane%16, 32 columns per
-// operand) written transposed, kt[k][token], as 8-byte vectors: select_op
-// MFMAs hand each lane 4 consecutive tokens of one key column.
-template <int K, int LD>
-__device__ __forceinline__ void store_kt(__bf16 (*kt)[LD], const bf8_t (&kA)[K / 32],
-                                         const bf8_t (&sel)[2]) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int l15 = lane & 15, lg = lane >> 4;
-#pragma unroll
-  for (int kk = 0; kk < K / 32; ++kk)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const f4_t c = mfma16(kA[kk], sel[h], f4_t{0.f, 0.f, 0.f, 0.f});
-      Vec<__bf16, 4> b;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) b.v[i] = static_cast<__bf16>(c[i]);
-      *reinterpret_cast<Vec<__bf16, 4>*>(&kt[kk * 32 + 16 * h + l15][wid * 16 + 4 * lg]) = b;
-    }
-}
-
 // (ah + al)(bh + bl) without the lo*lo term.
 __device__ __forceinline__ f4_t mfma_split3(const bf8_t& ah, const bf8_t& al, const bf8_t& bh,
                                             const bf8_t& bl, f4_t c) {
@@ -462,20 +422,6 @@ __device__ __forceinline__ bool locate_chunk(const P& p, int64_t c, int64_t& n, 
   s = a + ci * kC;
   L = static_cast<int>(min<int64_t>(kC, b - s));
   return true;
-}
-
-// Lane's MFMA operand of a 16-row slab of a [64 tokens x K] bf16 matrix in
-// global memory (token t of the slab at element (row0 + t) * row_stride +
-// col_off): row = r0 + (lane & 15), 8 elements from kk*32 + 8*(lane>>4).
-// Rows >= L repeat row L-1 of the same chunk (branch-free, so the load never
-// stalls the wave); every consumer zeroes or drops those rows.
-__device__ __forceinline__ bf8_t load_rows_op(const void* base, int64_t col_off, int64_t row0,
-                                              int L, int64_t row_stride, int r0, int kk) {
-  const int lane = threadIdx.x & 63;
-  const int r = min(r0 + (lane & 15), L - 1);
-  const bf16* src = reinterpret_cast<const bf16*>(base) + (row0 + r) * row_stride + col_off +
-                    kk * 32 + 8 * (lane >> 4);
-  return *reinterpret_cast<const bf8_t*>(src);
 }
 
 // 16x16x16 bf16 MFMA: lane l holds A[l%16][4(l/16)+e], B[4(l/16)+e][l%16]
