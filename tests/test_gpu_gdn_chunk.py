@@ -189,17 +189,20 @@ def test_rejects_non_bf16(dev):
         _run(dev, q, k, v, g, beta, h0, torch.tensor([0, 64], dtype=torch.int32), True)
 
 
-def test_v_tiles_and_scale(dev):
-    # V = 64 (two 32-column tiles), custom scale.
+@pytest.mark.parametrize("V", [64, 32, 96])
+def test_v_tiles_and_scale(dev, V):
+    # Custom scale and V other than 128.  V = 64 is one tile of the 512-lane
+    # state kernel; V = 32 and 96 are one and three 32-column tiles of the
+    # 256-lane kernel that serves V not a multiple of 64.
     from torch_npu_ops_amd import ops
     gen = torch.Generator().manual_seed(11)
     T, H, HV = 200, 2, 4
     q = torch.randn(1, T, H, 128, generator=gen).bfloat16()
     k = torch.randn(1, T, H, 128, generator=gen).bfloat16()
-    v = torch.randn(1, T, HV, 64, generator=gen).bfloat16()
+    v = torch.randn(1, T, HV, V, generator=gen).bfloat16()
     g = torch.log(torch.sigmoid(torch.randn(1, T, HV, generator=gen)))
     beta = torch.sigmoid(torch.randn(1, T, HV, generator=gen)).bfloat16()
-    h0 = torch.randn(1, HV, 128, 64, generator=gen)
+    h0 = torch.randn(1, HV, 128, V, generator=gen)
     cu = torch.tensor([0, T], dtype=torch.int32)
     _check(dev, q, k, v, g, beta, h0, cu, True, scale=0.25)
 
