@@ -222,13 +222,23 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_tok_kernel(RopeParams 
   constexpr int kCS = POS ? 1 : 2;
   float c[kCS][kVec], sn[kCS][kVec];
   if constexpr (POS) {
+    // Every team of the wave needs the same kHalf values: each lane forms
+    // cos / sin of dims ln, ln + 64, .. once (the same sincosf of the same
+    // arguments) and the teams read theirs from the wave's LDS table.
+    __shared__ __align__(16) float tab[4][2][kHalf];
+    const int w = threadIdx.x >> 6;
     const float pos = p.pos_is_i64
                           ? static_cast<float>(reinterpret_cast<const int64_t*>(p.pos)[tok])
                           : static_cast<float>(reinterpret_cast<const int32_t*>(p.pos)[tok]);
-    float f[kVec];
-    ld_f32<float, kVec>(p.inv_freq + d0, f);
 #pragma unroll
-    for (int u = 0; u < kVec; ++u) sincosf(pos * f[u], &sn[0][u], &c[0][u]);
+    for (int i = ln; i < kHalf; i += kWave) sincosf(pos * p.inv_freq[i], &tab[w][1][i], &tab[w][0][i]);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < kVec; ++u) {
+      c[0][u] = tab[w][0][d0 + u];
+      sn[0][u] = tab[w][1][d0 + u];
+    }
   } else {
     const A* cs = reinterpret_cast<const A*>(p.cos) + tok * p.stride_sc;
     const A* ss = reinterpret_cast<const A*>(p.sin) + tok * p.stride_sc;
