@@ -308,21 +308,6 @@ __global__ void __launch_bounds__(1024)
   }
 }
 
-int num_cus() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
-            hipSuccess ||
-        n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 template <typename T, typename WT, int VEC, int TPG, int NV, bool HAS_Z,
           bool FULL>
 int launch_tile_z(const NormParams& p, hipStream_t s) {

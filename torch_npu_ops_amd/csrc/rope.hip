@@ -79,19 +79,20 @@ __device__ __forceinline__ void st_f32(T* p, const float (&in)[N]) {
 // 4.15 us, G = 4 4.5 us (half the waves, each twice as long); staging the
 // block's cos/sin rows and weights in LDS instead (one small load per lane
 // and a barrier) took 4.7-4.9 us.  Issuing the x loads first, before the
-// q / k / v branch, was worth 0.5 us of the G = 2 gain.
+// q / k / v branch, was worth 0.5 us of the G = 2 gain.  The block size is
+// chosen at launch (a whole number of waves, blockDim.x / kTeam teams).
 template <typename T, typename A, int HD, int G>
-__global__ void __launch_bounds__(256) split_rmsnorm_rope_kernel(RopeParams p) {
+__global__ void __launch_bounds__(1024) split_rmsnorm_rope_kernel(RopeParams p) {
   constexpr int kHalf = HD / 2;
   constexpr int kVec = (16 / sizeof(T)) < kHalf ? (16 / sizeof(T)) : kHalf;
   constexpr int kTeam = kHalf / kVec;
-  static_assert(kTeam >= 1 && kTeam <= kWave, "team must fit a wave");
-  constexpr int kTeams = 256 / kTeam;
+  static_assert(kTeam >= 1 && kTeam <= kWave && kWave % kTeam == 0, "team must fit a wave");
+  const int teams = blockDim.x / kTeam;
 
   const int team = threadIdx.x / kTeam;
   const int lane = threadIdx.x % kTeam;
   const int groups = (p.hq + 2 * p.hkv) / G;
-  const int64_t slot = static_cast<int64_t>(blockIdx.x) * kTeams + team;
+  const int64_t slot = static_cast<int64_t>(blockIdx.x) * teams + team;
   if (slot >= p.T * groups) return;  // whole team exits together
   const int64_t tok = slot / groups;
   const int h = static_cast<int>(slot - tok * groups) * G;  // first head of the group
@@ -331,18 +332,25 @@ int launch_rope(const RopeParams& p, hipStream_t s) {
   }
   constexpr int kHalf = HD / 2;
   constexpr int kVec = (16 / sizeof(T)) < kHalf ? (16 / sizeof(T)) : kHalf;
-  constexpr int kTeams = 256 / (kHalf / kVec);
-  const int heads = p.hq + 2 * p.hkv;
-#define XK_ROPE_G(G)                                                                  \
-  hipLaunchKernelGGL((split_rmsnorm_rope_kernel<T, A, HD, G>),                        \
-                     dim3(cdiv(p.T * (heads / (G)), kTeams)), dim3(256), 0, s, p)
+  constexpr int kTeam = kHalf / kVec;
   // Two heads per team when both head counts are even, else one.
-  if (p.hq % 2 == 0 && p.hkv % 2 == 0) {
-    XK_ROPE_G(2);
-  } else {
-    XK_ROPE_G(1);
-  }
-#undef XK_ROPE_G
+  const int G = p.hq % 2 == 0 && p.hkv % 2 == 0 ? 2 : 1;
+  const int64_t teams = p.T * ((p.hq + 2 * p.hkv) / G);
+  if (teams == 0) return XK_OK;
+  // As many blocks as CUs (or a multiple, when one CU's share of the teams
+  // exceeds 1024 lanes), each the fewest whole waves that hold its share:
+  // every CU gets the same work.  At config 1 (6144 teams of 16 lanes) that
+  // is 256 blocks of 384 lanes: 3.99 us on MI355X, against 4.14 us for 384
+  // blocks of 256 lanes (1.5 blocks per CU) and 4.2 us for 512 of 192.
+  const int64_t cus = num_cus();
+  int64_t nb = cus;
+  while (cdiv(teams, nb) * kTeam > 1024) nb += cus;
+  const int64_t lanes = cdiv(cdiv(teams, nb) * kTeam, kWave) * kWave;
+  const dim3 grid(static_cast<unsigned>(cdiv(teams, lanes / kTeam)));
+  if (G == 2)
+    hipLaunchKernelGGL((split_rmsnorm_rope_kernel<T, A, HD, 2>), grid, dim3(lanes), 0, s, p);
+  else
+    hipLaunchKernelGGL((split_rmsnorm_rope_kernel<T, A, HD, 1>), grid, dim3(lanes), 0, s, p);
   return launch_status();
 }
 
