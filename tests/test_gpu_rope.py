@@ -156,6 +156,20 @@ def test_team_kernel_head_groups(dev, hq, hkv, mode):
     _check(out, ref, torch.bfloat16)
 
 
+# Team kernel just under the token-kernel threshold: with fp32 (16-lane
+# teams) one CU's share of the 24000 teams exceeds 1024 lanes, so the launch
+# uses two blocks per CU; bf16 with head_dim 64 has 4-lane teams.
+@pytest.mark.parametrize("dtype,hd", [(torch.float32, 128), (torch.bfloat16, 64)])
+def test_team_kernel_many_teams(dev, dtype, hd):
+    from torch_npu_ops_amd import ops
+    T, hq, hkv = 1000, 32, 8
+    qkv, qw, kw, pos, inv, cos, sin = _case(T, hq, hkv, hd, dtype, 21)
+    ref = orp.split_rmsnorm_rope(qkv, sin, cos, qw, kw, hq * hd, hkv * hd, hd, 1e-6)
+    out = ops.npu_split_rmsnorm_rope(qkv.to(dev), sin.to(dev), cos.to(dev), qw.to(dev),
+                                     kw.to(dev), hq * hd, hkv * hd, hd, 1e-6)
+    _check(out, ref, dtype)
+
+
 def test_single_token_and_empty(dev):
     from torch_npu_ops_amd import ops
     qkv, qw, kw, pos, inv, cos, sin = _case(1, 4, 4, 128, torch.bfloat16, 4)
