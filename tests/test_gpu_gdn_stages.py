@@ -122,6 +122,25 @@ def test_fwd_h(dev, cu_list):
     assert_state_close(fin.cpu(), rf)
 
 
+# V of 32, 64 and 96 (one, two and three 32-column tiles per head).
+@pytest.mark.parametrize("V", [32, 64, 96])
+def test_fwd_h_v_tiles(dev, V):
+    from torch_npu_ops_amd import ops
+    cu_list = [0, 1, 65, 130, 300]
+    _, k, v, g, beta, h0, cu = _inputs(cu_list)
+    v, h0 = v[..., :V].contiguous(), h0[..., :V].contiguous()
+    gc = og.chunk_local_cumsum(g.unsqueeze(0), cu)[0]
+    Ai = og.solve_tril(og.chunk_scaled_dot_kkt(k, beta, gc, cu), cu)
+    w, u = og.recompute_w_u(k, v, beta, gc, Ai, cu)
+    w, u = w.bfloat16(), u.bfloat16()
+    h, vnew, fin = ops.npu_chunk_gated_delta_rule_fwd_h(
+        _b(k, dev), _b(w, dev), _b(u, dev), _b(gc, dev), h0.to(dev), True, 64, True, cu.to(dev))
+    rh, rv, rf = og.chunk_fwd_h(k, w, u, gc, h0, cu)
+    torch.testing.assert_close(h[0].float().cpu(), rh, **O_TOL)
+    torch.testing.assert_close(vnew[0, :300].float().cpu(), rv[:300], **O_TOL)
+    assert_state_close(fin.cpu(), rf)
+
+
 def test_fwd_h_no_decay_no_state(dev):
     from torch_npu_ops_amd import ops
     _, k, v, g, beta, _, cu = _inputs([0, 70, 150])
