@@ -558,7 +558,7 @@ class GdnDecodeFusedCase(Case):
         from oracle import conv1d as oc
         from oracle import gdn as og
         a = self.inp
-        n = 16  # bounded sample: 16 of the 256 batch rows
+        n = a.B  # the whole batch
 
         def run():
             y, _ = oc.causal_conv1d_update(a.x[:n], a.cs[:n], a.cw, None, True,
@@ -569,7 +569,8 @@ class GdnDecodeFusedCase(Case):
             og.recurrent_gdn(q, k, v, a.gate[:n], a.beta[:n], a.K ** -0.5,
                              a.state[:n], T=1, ssm_state_indices=a.idx[:n],
                              dtype=torch.float32)
-        return run, f"{n} of 256 batch rows (conv update + split + l2norm + GDN step, fp32)", a.B / n
+        return run, ("the full config 5 call: all 256 batch rows (conv update + SiLU, split, "
+                     "l2norm, one GDN step; fp32)"), 1.0
 
 
 class GdnDecodeGatedCase(Case):
@@ -620,7 +621,7 @@ class GdnDecodeGatedCase(Case):
         from oracle import conv1d as oc
         from oracle import gating as ogt
         a = self.inp
-        n = 16  # bounded sample: 16 of the 256 batch rows
+        n = a.B  # the whole batch
 
         def run():
             y, _ = oc.causal_conv1d_update(a.x[:n], a.cs[:n], a.cw, None, True,
@@ -632,8 +633,8 @@ class GdnDecodeGatedCase(Case):
                 self.A_log, self.a[:n][None], self.dt_bias, q, k, v, self.b[:n][None],
                 a.state[:n], a.idx[:n], torch.arange(n + 1, dtype=torch.int32),
                 a.K ** -0.5, True, dtype=torch.float32)
-        return (run, f"{n} of 256 batch rows (conv update + split + gating + l2norm + "
-                "GDN step, fp32)", a.B / n)
+        return (run, "all 256 batch rows (conv update + split + gating + l2norm + GDN step, "
+                "fp32)", 1.0)
 
 
 class GdnRecurrentCase(Case):
@@ -680,13 +681,13 @@ class GdnRecurrentCase(Case):
     def cpu(self):
         from oracle import gdn as og
         a = self.inp
-        n = 16
+        n = a.B
 
         def run():
             og.recurrent_gdn(self.q[:n], self.k[:n], self.v[:n], a.gate[:n],
                              a.beta[:n], a.K ** -0.5, a.state[:n], T=1,
                              ssm_state_indices=a.idx[:n], dtype=torch.float32)
-        return run, f"{n} of 256 sequences, fp32", a.B / n
+        return run, "all 256 sequences, fp32", 1.0
 
 
 class GdnGatingCase(Case):
@@ -783,14 +784,14 @@ class GdnSigmoidGatingCase(Case):
     def cpu(self):
         from oracle import gating as ogt
         a = self.inp
-        n = 16
+        n = a.B
 
         def run():
             ogt.sigmoid_gating_delta_rule_update(
                 self.A_log, self.ga[:n], self.dt_bias, self.q[:n], self.k[:n], self.v[:n],
                 self.gb[:n], a.state[:n], a.idx[:n], torch.arange(n + 1, dtype=torch.int32),
                 a.K ** -0.5, True, dtype=torch.float32)
-        return run, f"{n} of 256 sequences, fp32", a.B / n
+        return run, "all 256 sequences, fp32", 1.0
 
 
 class QkvzbaSplitCase(Case):
@@ -852,7 +853,7 @@ class GdnChunkCase(Case):
               "128, chunk 64, q/k l2-normalised, g=-softplus(N(0,1)) fp32, "
               "beta=sigmoid(N(0,1)) bf16, h0~N(0,0.02) fp32, outputs o + final state")
     source = "gdn_chunk.hip"
-    kernel = "gdn_chunk_state_kernel"
+    kernel = "gdn_chunk_state8_kernel"
     T, NSEQ, H, HV, K, V = 16384, 8, 16, 32, 128, 128
     # q/k + v + o (bf16) + g (fp32) + beta (bf16) + h0/ht (fp32)
     algo_bytes = (T * H * K * 2 * 2 + T * HV * V * 2 * 2 + T * HV * (4 + 2)
@@ -922,15 +923,47 @@ class GdnChunkStagedCase(GdnChunkCase):
     source = "gdn_stages.hip"
     kernel = "chunk_fwd_h_kernel"
 
-    def sets(self, dev, n):
+    def nchunks(self):
+        lens = (self.cu[1:] - self.cu[:-1]).tolist()
+        return sum(-(-int(x) // 64) for x in lens)
+
+    def stage_io(self):
+        """(entry point, kernel, bytes of the stage's own inputs and outputs
+        at their dtypes) per stage, in pipeline order: the stage API keeps
+        its intermediates in HBM by definition, so each stage's roofline is
+        its own traffic."""
+        T, H, HV, K, V, N = self.T, self.H, self.HV, self.K, self.V, self.NSEQ
+        nt = self.nchunks()
+        cu = (N + 1) * 4
+        k_b = T * H * K * 2          # k (bf16), also q
+        v_b = T * HV * V * 2         # v, u, v_new, o (bf16)
+        w_b = T * HV * K * 2         # w (bf16)
+        g_b = T * HV * 4             # g, g_cumsum (fp32)
+        bt_b = T * HV * 2            # beta (bf16)
+        A_b = T * HV * 64 * 4        # A (fp32)
+        Ai_b = T * HV * 64 * 2       # Ai (bf16)
+        h_b = nt * HV * K * V * 2    # h snapshots (bf16)
+        s_b = N * HV * K * V * 4     # h0 / ht (fp32)
+        return [
+            ("chunk_local_cumsum", "chunk_cumsum_scan_kernel", 2 * g_b + cu),
+            ("chunk_scaled_dot_kkt", "chunk_kkt_kernel", k_b + bt_b + g_b + A_b + cu),
+            ("solve_tril", "solve_tril_kernel", A_b + Ai_b + cu),
+            ("recompute_w_u", "recompute_w_u_kernel",
+             k_b + v_b + bt_b + g_b + Ai_b + w_b + v_b + cu),
+            ("chunk_fwd_h", "chunk_fwd_h_kernel", k_b + w_b + v_b + g_b + 2 * s_b + h_b + v_b + cu),
+            ("chunk_fwd_o", "chunk_fwd_o_kernel", 2 * k_b + v_b + h_b + g_b + v_b + cu),
+        ]
+
+    def stage_sets(self, dev, n):
+        """n buffer sets, each a list of the six stage closures (in order)."""
         from torch_npu_ops_amd import _lib
         lib = _lib.lib()
         cu = self.cu.to(dev)
-        lens = (self.cu[1:] - self.cu[:-1]).tolist()
-        nt = sum(-(-int(x) // 64) for x in lens)
+        nt = self.nchunks()
         wsb = lib.xk_gdn_stage_workspace_bytes(self.NSEQ)
         T, H, HV, K, V = self.T, self.H, self.HV, self.K, self.V
         bf, f32 = torch.bfloat16, torch.float32
+        I32, BF, F32 = _lib.XK_I32, _lib.XK_BF16, _lib.XK_F32
         out = []
         for _ in range(n):
             q, k, v = self.q.to(dev), self.k.to(dev), self.v.to(dev)
@@ -945,32 +978,57 @@ class GdnChunkStagedCase(GdnChunkCase):
                 vn=torch.empty(T, HV, V, dtype=bf, device=dev),
                 ht=torch.empty_like(h0), o=torch.empty_like(v),
                 ws=torch.empty(wsb, dtype=torch.uint8, device=dev))
+            ws = b["ws"].data_ptr()
 
-            def run(q=q, k=k, v=v, g=g, beta=beta, h0=h0, b=b):
-                st = _cur_stream()
-                I32, BF, F32 = _lib.XK_I32, _lib.XK_BF16, _lib.XK_F32
-                ws, wsn = b["ws"].data_ptr(), wsb
+            def cumsum(g=g, b=b, ws=ws):
                 _ok(lib.xk_chunk_local_cumsum(g.data_ptr(), F32, b["gc"].data_ptr(), T, HV,
-                                              cu.data_ptr(), I32, self.NSEQ, 64, st), lib)
+                                              cu.data_ptr(), I32, self.NSEQ, 64, _cur_stream()),
+                    lib)
+
+            def kkt(k=k, beta=beta, b=b, ws=ws):
                 _ok(lib.xk_chunk_scaled_dot_kkt(k.data_ptr(), BF, beta.data_ptr(), BF,
                                                 b["gc"].data_ptr(), b["A"].data_ptr(), T, H, HV,
-                                                K, cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                                                K, cu.data_ptr(), I32, self.NSEQ, ws, wsb,
+                                                _cur_stream()), lib)
+
+            def tril(b=b, ws=ws):
                 _ok(lib.xk_solve_tril(b["A"].data_ptr(), b["Ai"].data_ptr(), BF, T, HV,
-                                      cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                                      cu.data_ptr(), I32, self.NSEQ, ws, wsb, _cur_stream()), lib)
+
+            def wu(k=k, v=v, beta=beta, b=b, ws=ws):
                 _ok(lib.xk_recompute_w_u(k.data_ptr(), v.data_ptr(), BF, beta.data_ptr(), BF,
                                          b["gc"].data_ptr(), b["Ai"].data_ptr(), BF,
                                          b["w"].data_ptr(), b["u"].data_ptr(), T, H, HV, K, V,
-                                         cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                                         cu.data_ptr(), I32, self.NSEQ, ws, wsb, _cur_stream()),
+                    lib)
+
+            def fwd_h(k=k, h0=h0, b=b, ws=ws):
                 _ok(lib.xk_chunk_fwd_h(k.data_ptr(), b["w"].data_ptr(), b["u"].data_ptr(), BF,
                                        b["gc"].data_ptr(), h0.data_ptr(), b["h"].data_ptr(), nt,
                                        b["vn"].data_ptr(), b["ht"].data_ptr(), T, H, HV, K, V,
-                                       cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                                       cu.data_ptr(), I32, self.NSEQ, ws, wsb, _cur_stream()),
+                    lib)
+
+            def fwd_o(q=q, k=k, b=b, ws=ws):
                 _ok(lib.xk_chunk_fwd_o(q.data_ptr(), k.data_ptr(), b["vn"].data_ptr(),
                                        b["h"].data_ptr(), nt, BF, b["gc"].data_ptr(),
                                        b["o"].data_ptr(), self.K ** -0.5, T, H, HV, K, V,
-                                       cu.data_ptr(), I32, self.NSEQ, ws, wsn, st), lib)
+                                       cu.data_ptr(), I32, self.NSEQ, ws, wsb, _cur_stream()),
+                    lib)
+            out.append([cumsum, kkt, tril, wu, fwd_h, fwd_o])
+        return out
+
+    def sets(self, dev, n):
+        out = []
+        for st in self.stage_sets(dev, n):
+            def run(st=st):
+                for f in st:
+                    f()
             out.append(run)
         return out
+
+    def cpu(self):
+        return None  # the same workload as gdn_chunk_prefill: its CPU line is reused
 
 
 class L2NormCase(Case):
@@ -1139,6 +1197,16 @@ def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
     if case.algo_bytes == 0:
         nsets = 2
     runs = case.sets(dev, nsets)
+    ms = time_runs(runs, dev, steps, warmup, eager)
+    del runs
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return ms
+
+
+def time_runs(runs, dev, steps: int, warmup: int, eager: bool):
+    """time_gpu's timing of closures that rotate over len(runs) buffer sets."""
+    nsets = len(runs)
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -1181,15 +1249,39 @@ def time_gpu(case: Case, dev, steps: int, warmup: int, eager: bool):
             reps.append(t0.elapsed_time(t1) / steps)
         ms = statistics.median(reps)
         del graph
-    del runs
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
     return ms
 
 
+def time_stages(case, dev, steps: int, warmup: int):
+    """Per-stage time (ms) of a staged case: every buffer set runs the whole
+    pipeline once (so each stage's inputs hold real intermediates), then
+    each stage is timed alone, eagerly, over the sets."""
+    nsets = max(2, min(MAX_SETS, -(-ROTATE_BYTES // max(case.algo_bytes, 1))))
+    sets = case.stage_sets(dev, nsets)
+    for st in sets:
+        for f in st:
+            f()
+    torch.cuda.synchronize()
+    out = []
+    for i in range(len(sets[0])):
+        out.append(time_runs([st[i] for st in sets], dev, steps, warmup, True))
+    del sets
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def time_cpu(case: Case):
+    """(seconds per full call, sample description, runs, scale) of the op's
+    CPU baseline: one warm-up, then the median of at least three timed runs
+    (up to five within 20 s), times `scale` when the closure runs a stated
+    sample of the call (scale 1: the whole call is timed).  None when the
+    case has no CPU closure of its own."""
     torch.set_num_threads(cpu_threads())
-    run, sample, scale = case.cpu()
+    got = case.cpu()
+    if got is None:
+        return None
+    run, sample, scale = got
     run()  # warm-up
     ts = []
     budget_end = time.perf_counter() + 20.0
@@ -1199,7 +1291,28 @@ def time_cpu(case: Case):
         ts.append(time.perf_counter() - t)
         if time.perf_counter() > budget_end:
             break
-    return statistics.median(ts) * scale, sample, len(ts)
+    return statistics.median(ts) * scale, sample, len(ts), scale
+
+
+def cpu_line(case: Case, gpu_us: float):
+    """The op line's cpu_baseline object (None if the case has no CPU
+    closure)."""
+    got = time_cpu(case)
+    if got is None:
+        return None
+    sec, sample, nrun, scale = got
+    per_tok = getattr(case, "tokens", 0)
+    line = {"value": round(per_tok / sec) if per_tok else round(case.algo_bytes / sec / 1e9, 3),
+            "unit": "tokens/s" if per_tok else "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": sample, "scale": scale, "runs": nrun,
+            "ms_per_call": round(sec * 1e3, 3),
+            "gpu_speedup": round(sec * 1e6 / gpu_us, 1),
+            **cpu_host()}
+    print(f"[bench] cpu baseline {case.name}: {sec*1e3:.1f} ms/call"
+          + (f" (sample x {scale:g})" if scale != 1.0 else " (whole call)"),
+          file=sys.stderr, flush=True)
+    return line
 
 
 def source_sha(fname):
@@ -1294,7 +1407,7 @@ def floors(dev, steps, warmup, moved_list):
 # ---------------------------------------------------------------------------
 PROFILE_COMMANDS = [
     ("trace", "rocprofv3 --kernel-trace --stats -f csv -d <out>/trace -o run -- "
-              "python3 <repo>/bench.py --no-cpu"),
+              "python3 <repo>/bench.py > <out>/trace_bench.json"),
     ("FETCH_SIZE", "rocprofv3 --pmc FETCH_SIZE -f csv -d <out>/FETCH_SIZE -o p -- "
                    "python3 <repo>/bench.py --no-cpu --eager --steps 3 --warmup 1"),
     ("WRITE_SIZE", "rocprofv3 --pmc WRITE_SIZE -f csv -d <out>/WRITE_SIZE -o p -- "
@@ -1304,6 +1417,13 @@ PROFILE_COMMANDS = [
     ("copy_WRITE_SIZE", "rocprofv3 --pmc WRITE_SIZE -f csv -d <out>/copy_WRITE_SIZE -o p -- "
                         "python3 <repo>/bench.py --copy-calibration --steps 5"),
 ]
+
+# Kernels of each multi-kernel op, in launch order (per-call time against the
+# sum of their per-dispatch medians).
+OP_KERNELS = {
+    "gdn_chunk_prefill": ["chunk_offsets_kernel<ChunkParams>", "gdn_chunk_prep_kernel",
+                          "gdn_chunk_state8_kernel"],
+}
 
 
 def kernel_label(raw):
@@ -1330,6 +1450,27 @@ def kernel_label(raw):
     return raw[:50]
 
 
+def _trace_durations(out_dir):
+    """Per-dispatch kernel durations (us) by kernel label, from the
+    --kernel-trace CSV of the trace run."""
+    import csv
+    import collections
+    dur = collections.defaultdict(list)
+    path = glob_one(os.path.join(out_dir, "trace", "**", "run_kernel_trace.csv"))
+    for r in csv.DictReader(open(path)):
+        dur[kernel_label(r["Kernel_Name"])].append(
+            (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return dur
+
+
+def glob_one(pattern):
+    import glob
+    hits = sorted(glob.glob(pattern, recursive=True))
+    if not hits:
+        raise FileNotFoundError(pattern)
+    return hits[0]
+
+
 def summarize_profile(out_dir):
     """Writes profiles/kernel_durations_all_configs.md,
     profiles/hbm_traffic_all_configs.md and TRAFFIC_JSON from the rocprofv3
@@ -1337,15 +1478,22 @@ def summarize_profile(out_dir):
     import csv
     import collections
     import glob
+    dur = _trace_durations(out_dir)
     stats = []
-    for r in csv.DictReader(open(os.path.join(out_dir, "trace", "run_kernel_stats.csv"))):
-        stats.append((kernel_label(r["Name"]), int(r["Calls"]), float(r["AverageNs"]) / 1e3,
-                      float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3))
+    for k, v in dur.items():
+        stats.append((k, len(v), statistics.median(v), statistics.mean(v), min(v), max(v)))
     stats.sort(key=lambda x: -x[2])
+    bench_line = None
+    bpath = os.path.join(out_dir, "trace_bench.json")
+    if os.path.exists(bpath):
+        for ln in open(bpath):
+            if ln.startswith("{"):
+                bench_line = json.loads(ln)
 
     def pmc(sub, counter):
         acc = collections.defaultdict(list)
-        for r in csv.DictReader(open(os.path.join(out_dir, sub, "p_counter_collection.csv"))):
+        for r in csv.DictReader(open(glob_one(os.path.join(out_dir, sub, "**",
+                                                           "p_counter_collection.csv")))):
             if r["Counter_Name"] == counter:
                 acc[kernel_label(r["Kernel_Name"])].append(float(r["Counter_Value"]))
         return {k: statistics.mean(v) for k, v in acc.items()}
@@ -1360,6 +1508,10 @@ def summarize_profile(out_dir):
     for c in CASES.values():
         kernel_ops[c.kernel].append(c.name)
         algo.setdefault(c.kernel, []).append(c.algo_bytes)
+    for op, ks in OP_KERNELS.items():
+        for k in ks:
+            if op not in kernel_ops[k]:
+                kernel_ops[k].append(op)
     traffic = {k: fetch[k] * 1024 * ff + write[k] * 1024 * wf
                for k in fetch if k in write}
     csrc = os.path.join(REPO, "torch_npu_ops_amd", "csrc")
@@ -1370,18 +1522,39 @@ def summarize_profile(out_dir):
                    "traffic_bytes": traffic}, f, indent=1)
     prof = os.path.join(REPO, "profiles")
     cmds = dict(PROFILE_COMMANDS)
+    ops = bench_line["ops"] if bench_line else {}
     with open(os.path.join(prof, "kernel_durations_all_configs.md"), "w") as f:
         f.write("# Kernel durations, all BASELINE configs\n\nCommand (repo root on the GPU box; "
                 "`cd /tmp && export TMPDIR=/tmp` first):\n\n    " + cmds["trace"] + "\n\n"
-                "bench.py's default timing per op (clock-settle phase, warm-up, 3 x 50 timed "
-                "calls on buffer sets rotated past the Infinity Cache; small ops graph-replayed, "
-                "plus their same-traffic copies).  Averages are rocprofv3's per-dispatch kernel "
-                "durations over every dispatch, settle phase included.  Summarised by "
-                "`python3 bench.py --summarize-profile <out>`.\n\n"
-                "| kernel | calls | avg us | min us | max us | bench ops |\n|---|---|---|---|---|---|\n")
-        for k, c, a, mn, mx in stats:
-            f.write(f"| {k} | {c} | {a:.2f} | {mn:.2f} | {mx:.2f} | "
-                    f"{', '.join(kernel_ops.get(k, [])) or '-'} |\n")
+                "bench.py's default run (clock-settle phase, warm-up, 3 x 50 timed calls per op "
+                "on buffer sets rotated past the Infinity Cache; small ops graph-replayed, plus "
+                "their same-traffic copies; the stage-by-stage line also times each stage alone).  "
+                "Per-dispatch durations come from the kernel-trace CSV; the median is the "
+                "steady-state figure (the first tens of dispatches of an op run before the "
+                "clocks settle).  The last column is the per-call time that the same run's bench "
+                "line reports (HIP events around back-to-back calls), so both come from one "
+                "process on one box.  Summarised by `python3 bench.py --summarize-profile "
+                "<out>`.\n\n"
+                "| kernel | dispatches | median us | mean us | min us | max us | bench ops | "
+                "bench us per call (same run) |\n|---|---|---|---|---|---|---|---|\n")
+        for k, c, med, mean, mn, mx in stats:
+            names = kernel_ops.get(k, [])
+            per_call = ", ".join(f"{ops[n]['us_per_call']:.2f}" for n in names if n in ops)
+            f.write(f"| {k} | {c} | {med:.2f} | {mean:.2f} | {mn:.2f} | {mx:.2f} | "
+                    f"{', '.join(names) or '-'} | {per_call or '-'} |\n")
+        for op, ks in OP_KERNELS.items():
+            if all(k in dur for k in ks) and op in ops:
+                meds = [statistics.median(dur[k]) for k in ks]
+                f.write(f"\n{op}: the per-dispatch medians of its kernels ("
+                        + " + ".join(f"{k} {m:.2f}" for k, m in zip(ks, meds))
+                        + f") sum to {sum(meds):.2f} us; the same run's bench line measures "
+                        f"{ops[op]['us_per_call']:.2f} us per call.\n")
+        if bench_line:
+            f.write("\nThe same run's bench line (per op: us per call and fraction of the HBM "
+                    "peak):\n\n| op | us per call | GB/s | frac |\n|---|---|---|---|\n")
+            for n, o in ops.items():
+                f.write(f"| {n} | {o['us_per_call']:.2f} | {o['GB/s']:.1f} | "
+                        f"{o['roofline']['frac']:.4f} |\n")
     with open(os.path.join(prof, "hbm_traffic_all_configs.md"), "w") as f:
         f.write("# HBM traffic per dispatch vs algorithmic bytes, all BASELINE configs\n\n"
                 "Commands (repo root on the GPU box; `cd /tmp && export TMPDIR=/tmp` first; "
@@ -1406,6 +1579,13 @@ def summarize_profile(out_dir):
             alg = f"{statistics.mean(a) / 1e6:.1f} ({', '.join(kernel_ops[k])})" if a else "-"
             f.write(f"| {k} | {fetch[k]:.0f} | {write[k]:.0f} | {traffic[k] / 1e6:.1f} | {alg} | "
                     f"{ratio} |\n")
+        for op, ks in OP_KERNELS.items():
+            if all(k in traffic for k in ks) and op in CASES:
+                tot = sum(traffic[k] for k in ks)
+                f.write(f"\n{op}: its kernels move {tot / 1e6:.1f} MB in all ("
+                        + " + ".join(f"{k} {traffic[k] / 1e6:.1f}" for k in ks)
+                        + f"), {tot / CASES[op].algo_bytes:.3f} x the op's "
+                        f"{CASES[op].algo_bytes / 1e6:.1f} MB of algorithmic bytes.\n")
     print(f"[bench] wrote profiles/ summaries from {out_dir}", file=sys.stderr)
 
 
@@ -1497,6 +1677,19 @@ def main():
             tus = time_gpu(TailFloorCase(*tail), dev, args.steps, args.warmup, False) * 1e3
             ops[name]["strided_tail_floor_us"] = round(tus, 2)
             ops[name]["vs_strided_tail_floor"] = round(ms * 1e3 / tus, 3)
+        if hasattr(case, "stage_sets"):
+            # Each stage alone, against the roofline of its own inputs and
+            # outputs (the stage API keeps its intermediates in HBM).
+            st_ms = time_stages(case, dev, args.steps, args.warmup)
+            stages = []
+            for (entry, kern, io), sm in zip(case.stage_io(), st_ms):
+                sg = io / (sm * 1e-3) / 1e9
+                stages.append({"entry_point": entry, "kernel": kern, "us_per_call": round(sm * 1e3, 2),
+                               "own_io_bytes": io, "GB/s": round(sg, 1),
+                               "frac_of_own_io_roofline": round(sg / HBM_PEAK_GBS, 4)})
+                print(f"[bench]   stage {entry}: {sm*1e3:.2f} us, {io/1e6:.1f} MB own I/O, "
+                      f"{sg / HBM_PEAK_GBS:.1%} of peak", file=sys.stderr, flush=True)
+            ops[name]["stages"] = stages
         print(f"[bench] {name}: {ms*1e3:.2f} us/call, {gbs:.0f} GB/s "
               f"({gbs / HBM_PEAK_GBS:.1%} of peak)"
               + (f", {ops[name]['tokens/s']:.3g} tokens/s, "
@@ -1506,26 +1699,23 @@ def main():
     case = CASES[headline]()
     cpu = None
     if not args.no_cpu:
-        sec, sample, nrun = time_cpu(case)
-        per_tok = getattr(case, "tokens", 0)
-        cpu = {"value": round(per_tok / sec) if per_tok else round(case.algo_bytes / sec / 1e9, 2),
-               "unit": "tokens/s" if per_tok else "GB/s",
-               "cores": torch.get_num_threads(), "kind": "port",
-               "sample": f"{sample}; median of {nrun} runs, {sec*1e3:.1f} ms/call",
-               **cpu_host()}
-        print(f"[bench] cpu baseline {headline}: {sec*1e3:.1f} ms/call",
-              file=sys.stderr, flush=True)
-        # The chunked prefill's target is stated against its CPU tokens/s.
-        if GdnChunkCase.name in ops and headline != GdnChunkCase.name:
-            csec, csample, cn = time_cpu(GdnChunkCase())
-            ops[GdnChunkCase.name]["cpu_baseline"] = {
-                "value": round(GdnChunkCase.tokens / csec), "unit": "tokens/s",
-                "cores": torch.get_num_threads(), "kind": "port",
-                "sample": f"{csample}; median of {cn} runs, scaled to the full "
-                          f"config: {csec*1e3:.0f} ms/call",
-                **cpu_host()}
-            print(f"[bench] cpu baseline {GdnChunkCase.name}: {csec*1e3:.0f} ms/call",
-                  file=sys.stderr, flush=True)
+        # The CPU restatement of each op's reference on the same inputs, on
+        # this host's cores, after every GPU measurement.
+        for name in names:
+            c = CASES[name]()
+            line = cpu_line(c, ops[name]["us_per_call"])
+            if line is None and name == GdnChunkStagedCase.name and \
+                    GdnChunkCase.name in ops and "cpu_baseline" in ops[GdnChunkCase.name]:
+                line = dict(ops[GdnChunkCase.name]["cpu_baseline"],
+                            sample="the gdn_chunk_prefill line's CPU run (same workload)")
+                line["gpu_speedup"] = round(line["ms_per_call"] * 1e3 / ops[name]["us_per_call"], 1)
+            if line is None and name == GdnChunkStagedCase.name:
+                c = GdnChunkCase()
+                line = cpu_line(c, ops[name]["us_per_call"])
+            if line is not None:
+                ops[name]["cpu_baseline"] = line
+            del c
+        cpu = ops[headline].get("cpu_baseline")
     traffic = measured_traffic(case)
     line = {
         "metric": "achieved HBM GB/s (% of peak) per op; chunked GDN prefill tokens/s",

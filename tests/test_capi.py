@@ -53,16 +53,24 @@ def test_empty_input_is_a_no_op_without_gpu():
 
 def test_noalloc_chunk_rejects_problems_beyond_its_scratch_without_gpu():
     # 64 MiB of static scratch: 100k tokens at 32 v-heads need ~2 GB of
-    # records, so the call is refused before any GPU work.
+    # records, so the call is refused before any GPU work.  The pointers are
+    # placeholders (aligned, never dereferenced: the entry point checks the
+    # arguments, then the size, before it touches the device).
     lib = _lib.lib()
     need = lib.xk_gdn_chunk_workspace_bytes(100_000, 8, 32)
     assert need > 64 << 20
-    st = lib.xk_gdn_chunk_fwd_noalloc(
-        None, None, None, _lib.XK_BF16, None, _lib.XK_F32, None, _lib.XK_BF16, None, None,
-        None, None, _lib.XK_I32, 8, 100_000, 16, 32, 128, 128, 0.1, 1, None)
+    fake = 1 << 20
+
+    def call(N, T, H=16, HV=32, dtype=_lib.XK_BF16, ptr=fake):
+        return lib.xk_gdn_chunk_fwd_noalloc(
+            ptr, ptr, ptr, dtype, ptr, _lib.XK_F32, ptr, _lib.XK_BF16, ptr, None,
+            None, ptr, _lib.XK_I32, N, T, H, HV, 128, 128, 0.1, 1, None)
+    st = call(8, 100_000)
     assert st == _lib.XK_ERR_SCRATCH
     assert "static scratch" in _lib.status_string(st)
-    st = lib.xk_gdn_chunk_fwd_noalloc(
-        None, None, None, _lib.XK_BF16, None, _lib.XK_F32, None, _lib.XK_BF16, None, None,
-        None, None, _lib.XK_I32, -1, 100, 16, 32, 128, 128, 0.1, 1, None)
-    assert st == _lib.XK_ERR_INVALID
+    # The same argument checks as xk_gdn_chunk_fwd come first.
+    assert call(-1, 100) == _lib.XK_ERR_INVALID
+    assert call(8, 100_000, H=3) == _lib.XK_ERR_INVALID          # HV % H != 0
+    assert call(8, 100_000, dtype=_lib.XK_F32) == _lib.XK_ERR_UNSUPPORTED
+    assert call(8, 100_000, ptr=None) == _lib.XK_ERR_INVALID     # NULL inputs
+    assert call(0, 0, ptr=None) == _lib.XK_OK                    # no work

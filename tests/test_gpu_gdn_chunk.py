@@ -58,7 +58,7 @@ def _check(dev, q, k, v, g, beta, h0, cu, l2norm, scale=None, heads=None):
         o, ref_o = o[:, :, heads], ref_o[:, :, heads]
         fin, ref_s = fin[:, heads], ref_s[:, heads]
     torch.testing.assert_close(o, ref_o, **O_TOL)
-    print(f"final-state error / (RMS + |ref|): {state_error(fin, ref_s):.3e}", flush=True)
+    print(f"final-state error / (atol + rtol |ref|): {state_error(fin, ref_s):.3e}", flush=True)
     assert_state_close(fin, ref_s)
 
 

@@ -165,9 +165,47 @@ def build_torch_api(jobs: int | None = None, verbose: bool = True) -> str:
     return TORCH_API_PATH
 
 
+CONSUMER_SRC = os.path.join(REPO_DIR, "tests", "cpp", "api_consumer.cpp")
+CONSUMER_PATH = os.path.join(REPO_DIR, "tests", "cpp", "xk_api_consumer")
+
+
+def build_api_consumer(verbose: bool = True) -> str:
+    """tests/cpp/xk_api_consumer: a C++ executable (no Python) that links the
+    drop-in layer's objects (torch_api.cpp, registry.cpp, compiled by
+    build_torch_api), libxk.so and libtorch, as an engine would.  Its NEEDED
+    list names the torch libraries before libxk.so, so that the loader maps
+    PyTorch's HIP runtime first and libxk.so binds to it by soname."""
+    import torch
+    torch_dir = os.path.dirname(torch.__file__)
+    torch_lib = os.path.join(torch_dir, "lib")
+    cxx = os.environ.get("CXX", "g++")
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    obj = os.path.join(BUILD_DIR, "api_consumer.o")
+    _run([cxx, "-O2", "-std=c++17", "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+          f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+          f"-I{os.path.join(torch_dir, 'include')}",
+          f"-I{os.path.join(torch_dir, 'include', 'torch', 'csrc', 'api', 'include')}",
+          "-I/opt/rocm/include", f"-I{INCLUDE_DIR}", f"-I{TORCH_API_DIR}",
+          "-Wno-deprecated-declarations", "-c", CONSUMER_SRC, "-o", obj])
+    api_objs = [os.path.join(BUILD_DIR, "torch_api_" + n + ".o")
+                for n in ("torch_api.cpp", "registry.cpp")]
+    rel = os.path.relpath(PKG_DIR, os.path.dirname(CONSUMER_PATH))
+    tmp = CONSUMER_PATH + ".tmp"
+    _run([cxx, obj, *api_objs, "-o", tmp,
+          f"-L{torch_lib}", f"-L{PKG_DIR}",
+          f"-Wl,-rpath,{torch_lib}", f"-Wl,-rpath,$ORIGIN/{rel}",
+          "-Wl,--no-as-needed", "-ltorch", "-ltorch_cpu", "-lc10", "-lc10_hip", "-ltorch_hip",
+          "-lxk", "-Wl,--as-needed"])
+    os.replace(tmp, CONSUMER_PATH)
+    if verbose:
+        print(f"[xk build] linked {CONSUMER_PATH}", flush=True)
+    return CONSUMER_PATH
+
+
 def build_all(verbose: bool = True) -> None:
     build_lib(verbose=verbose)
     build_torch_api(verbose=verbose)
+    build_api_consumer(verbose=verbose)
     build_measure_lib(verbose=verbose)
 
 

@@ -31,9 +31,15 @@
 // previous inputs in a register window, so every x element is read from
 // HBM once (plus a W-1 token halo per tile, served from L2) and every output
 // written once.  Sequence boundaries inside a tile restart the window from
-// the sequence's state history.  The final-state update is a second, tiny
-// kernel so that no block can overwrite a slot another block still reads
-// as history.
+// the sequence's state history.  Prefill is one launch: tile edges are
+// moved so that every token whose window reaches into a sequence's state
+// history lies in the tile of the sequence's first token, and the lane that
+// reads that history (for its channels) writes the sequence's final state
+// after its token loop.  An output slot that is also the sequence's input
+// slot is thus overwritten only after it was read.  This needs tiles longer
+// than the history (kTileT > W - 1, asserted below) and no sequence whose
+// output slot is another sequence's input slot in the same call (the
+// reference kernel has the same requirement; include/xk_ops.h states it).
 #include "xk_common.h"
 
 namespace xk {
@@ -251,6 +257,10 @@ __device__ __forceinline__ int find_seq(const int32_t* qsl, int B, int64_t t) {
 #define XK_CONV_TILE_T 16
 #endif
 constexpr int kTileT = XK_CONV_TILE_T;
+// Widths up to 8 (the entry point's limit) leave a history of up to 7
+// inputs; the one-launch state write needs every tile to be longer than
+// that (see tile_edge in the kernel).
+static_assert(kTileT >= 8, "conv1d prefill tiles must be longer than the conv history");
 #ifndef XK_CONV_GROUP
 #define XK_CONV_GROUP 8
 #endif

@@ -89,7 +89,7 @@ struct ChunkParams {
   int32_t* chunk_off;  // [N+1] workspace
   int32_t* seq_order;  // [N] workspace: sequences, longest first
   int2* ctab;          // [NTmax] workspace: (first token, length) per chunk
-  bf16* dump;          // [64 * 32] workspace: sink for padded-row stores
+  bf16* dump;          // [64 * kBVMax] workspace: sink for padded-row stores
   char* rec;           // [NTmax, HV] records of kRec bytes, workspace
   int64_t N, NTmax;
   int64_t T;  // token rows of q/k/v
@@ -1018,13 +1018,19 @@ extern "C" int64_t xk_gdn_chunk_workspace_bytes(int64_t total_tokens, int64_t nu
          nt * HV * kRec;
 }
 
-extern "C" int xk_gdn_chunk_fwd(
-    const void* q, const void* k, const void* v, xk_dtype dtype, const void* g,
-    xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype, void* o,
-    const float* initial_state, float* final_state, const void* cu_seqlens,
-    xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
-    int64_t K, int64_t V, float scale, int use_qk_l2norm, void* workspace,
-    size_t workspace_bytes, void* stream) {
+namespace xk {
+namespace {
+
+// Argument checks shared by xk_gdn_chunk_fwd and xk_gdn_chunk_fwd_noalloc
+// (everything but the workspace).  *empty is set for a call with no work
+// (N or total_tokens 0), which returns XK_OK before its pointers are
+// checked.
+int chunk_args_status(const void* q, const void* k, const void* v, xk_dtype dtype,
+                      const void* g, xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype,
+                      const void* o, const void* cu_seqlens, xk_dtype cu_dtype, int64_t N,
+                      int64_t total_tokens, int64_t H, int64_t HV, int64_t K, int64_t V,
+                      bool* empty) {
+  *empty = false;
   if (N < 0 || total_tokens < 0 || H <= 0 || HV <= 0 || HV % H != 0)
     return XK_ERR_INVALID;
   // bf16 only, as the reference entry point (q/k feed the bf16 MFMA as-is).
@@ -1036,12 +1042,32 @@ extern "C" int xk_gdn_chunk_fwd(
   // Row pitches of q / k and v / o in bytes feed 24-bit multiplies.
   if (H * K * 2 >= (int64_t{1} << 24) || HV * V * 2 >= (int64_t{1} << 24))
     return XK_ERR_UNSUPPORTED;
-  if (N == 0 || total_tokens == 0) return XK_OK;
+  if (N == 0 || total_tokens == 0) {
+    *empty = true;
+    return XK_OK;
+  }
   // Token indices travel as int32 in the chunk table.
   if (total_tokens > INT32_MAX - kC) return XK_ERR_UNSUPPORTED;
   if (!q || !k || !v || !g || !beta || !o || !cu_seqlens) return XK_ERR_INVALID;
   if (!aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) || !aligned(o, 8))
     return XK_ERR_INVALID;
+  return XK_OK;
+}
+
+}  // namespace
+}  // namespace xk
+
+extern "C" int xk_gdn_chunk_fwd(
+    const void* q, const void* k, const void* v, xk_dtype dtype, const void* g,
+    xk_dtype g_dtype, const void* beta, xk_dtype beta_dtype, void* o,
+    const float* initial_state, float* final_state, const void* cu_seqlens,
+    xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
+    int64_t K, int64_t V, float scale, int use_qk_l2norm, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  bool empty = false;
+  const int ast = chunk_args_status(q, k, v, dtype, g, g_dtype, beta, beta_dtype, o, cu_seqlens,
+                                    cu_dtype, N, total_tokens, H, HV, K, V, &empty);
+  if (ast != XK_OK || empty) return ast;
   const int64_t need = xk_gdn_chunk_workspace_bytes(total_tokens, N, HV);
   if (!workspace || static_cast<int64_t>(workspace_bytes) < need) return XK_ERR_WORKSPACE;
   if (!aligned(workspace, 256)) return XK_ERR_WORKSPACE;
@@ -1130,10 +1156,14 @@ extern "C" int xk_gdn_chunk_fwd_noalloc(
     const float* initial_state, float* final_state, const void* cu_seqlens,
     xk_dtype cu_dtype, int64_t N, int64_t total_tokens, int64_t H, int64_t HV,
     int64_t K, int64_t V, float scale, int use_qk_l2norm, void* stream) {
+  // The same argument checks as xk_gdn_chunk_fwd, before the size check.
+  bool empty = false;
+  const int ast = chunk_args_status(q, k, v, dtype, g, g_dtype, beta, beta_dtype, o, cu_seqlens,
+                                    cu_dtype, N, total_tokens, H, HV, K, V, &empty);
+  if (ast != XK_OK || empty) return ast;
   const int64_t need = xk_gdn_chunk_workspace_bytes(total_tokens, N, HV);
   if (need < 0) return XK_ERR_INVALID;
   if (need > kNoAllocScratchBytes) return XK_ERR_SCRATCH;
-  if (N == 0 || total_tokens == 0) return XK_OK;
   void* ws = nullptr;
   const int st = scratch_on_current_device(static_cast<hipStream_t>(stream), &ws);
   if (st != XK_OK) return st;
