@@ -1606,6 +1606,10 @@ def main():
     ap.add_argument("--summarize-profile", metavar="OUT",
                     help="summarise the rocprofv3 output of PROFILE_COMMANDS under OUT into "
                          "profiles/ (no GPU needed)")
+    ap.add_argument("--copy-bytes", type=int, default=0, metavar="B",
+                    help="only time a plain device copy moving B bytes (B/2 read, B/2 "
+                         "written), eagerly, rotated past the Infinity Cache like the ops, "
+                         "and print it as JSON (a same-traffic reference for counter runs)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run plain 256 MiB device copies (the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -1624,6 +1628,12 @@ def main():
     dev = torch.device("cuda:0")
     if args.copy_calibration:
         copy_calibration(dev, args.steps)
+        return
+    if args.copy_bytes:
+        c = CopyFloorCase(args.copy_bytes)
+        us = time_gpu(c, dev, args.steps, args.warmup, True) * 1e3
+        print(json.dumps({"copy_bytes": c.algo_bytes, "timing": "eager", "us_per_call": round(us, 2),
+                          "GB/s": round(c.algo_bytes / (us * 1e-6) / 1e9, 1)}))
         return
     if args.floors:
         small = [c for c in CASES.values() if c.timing == "graph"]

@@ -126,6 +126,104 @@ __global__ void __launch_bounds__(kTh) chunk_cumsum_scan_kernel(CumsumParams p) 
   if (t < p.T) p.out[t * p.H + h] = x;
 }
 
+// Chunk size 64, up to kTileMaxHeads heads and kScanLdsSeqs sequences: one
+// block per chunk.  A chunk's g rows [s, s + L) x H are contiguous, so the
+// block loads them with coalesced reads into an LDS tile, each wave scans
+// whole heads down the tile (lane = token), and the block stores the tile
+// back with coalesced writes: every g read once and every output written
+// once.  The chunk_cumsum_scan_kernel layout (a wave per 64-token block and
+// head) reads with a stride of H values between lanes and re-reads the
+// prefix of a chunk that starts before its block: 5x the op's bytes in HBM
+// traffic at the prefill shape (16384 tokens x 32 heads) on MI355X.  Blocks
+// past the last chunk zero the tokens outside every sequence, 64 at a time,
+// as the other kernels do.
+constexpr int kTileMaxHeads = 64;
+
+template <typename GT>
+__global__ void __launch_bounds__(kTh) chunk_cumsum_tile_kernel(CumsumParams p) {
+  __shared__ int64_t scu[kScanLdsSeqs + 1];
+  __shared__ int32_t soff[kScanLdsSeqs + 1];
+  __shared__ float tile[kC][kTileMaxHeads + 1];
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1), wid = tid >> 6;
+  for (int64_t i = tid; i <= p.N; i += kTh) scu[i] = cu_at(p, i);
+  __syncthreads();
+  // Chunks of sequence n (none for an empty or malformed, decreasing, entry).
+  auto nchunks = [&](int64_t n) {
+    const int64_t len = scu[n + 1] - scu[n];
+    return static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+  };
+  if (wid == 0) {
+    // Chunk offsets: lane l sums the chunk counts of its run of sequences,
+    // then an exclusive wave scan places the runs.
+    const int64_t per = (p.N + kWave - 1) / kWave;
+    const int64_t b0 = lane * per, b1 = min(p.N, b0 + per);
+    int32_t sum = 0;
+    for (int64_t n = b0; n < b1; ++n) sum += nchunks(n);
+    int32_t incl = sum;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int32_t t = __shfl_up(incl, o, kWave);
+      if (lane >= o) incl += t;
+    }
+    int32_t acc = incl - sum;
+    for (int64_t n = b0; n < b1; ++n) {
+      soff[n] = acc;
+      acc += nchunks(n);
+    }
+    if (lane == kWave - 1) soff[p.N] = incl;
+  }
+  __syncthreads();
+  const int H = p.H;
+  const int64_t b = blockIdx.x;
+  const int64_t total = soff[p.N];
+  int64_t s;
+  int L;
+  bool zero = false;
+  if (b < total) {
+    int64_t lo = 0, hi = p.N;  // soff[lo] <= b < soff[hi]
+    while (hi - lo > 1) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (soff[mid] <= b) lo = mid; else hi = mid;
+    }
+    s = scu[lo] + (b - soff[lo]) * kC;
+    L = static_cast<int>(min<int64_t>(kC, scu[lo + 1] - s));
+  } else {
+    // Tokens [0, cu[0]) and [cu[N], T) belong to no sequence.
+    const int64_t z = b - total;
+    const int64_t head_tiles = (scu[0] + kC - 1) / kC;
+    if (z < head_tiles) {
+      s = z * kC;
+      L = static_cast<int>(min<int64_t>(kC, scu[0] - s));
+    } else {
+      s = scu[p.N] + (z - head_tiles) * kC;
+      if (s >= p.T) return;  // whole block
+      L = static_cast<int>(min<int64_t>(kC, p.T - s));
+    }
+    zero = true;
+  }
+  const int n_el = L * H;
+  const GT* g = reinterpret_cast<const GT*>(p.g) + s * H;
+  float* out = p.out + s * H;
+  if (zero) {
+    for (int i = tid; i < n_el; i += kTh) out[i] = 0.f;
+    return;
+  }
+  for (int i = tid; i < n_el; i += kTh) tile[i / H][i % H] = to_f32(g[i]);
+  __syncthreads();
+  for (int h = wid; h < H; h += kTh / kWave) {
+    float x = lane < L ? tile[lane][h] : 0.f;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const float y = __shfl_up(x, o, kWave);
+      if (lane >= o) x += y;
+    }
+    if (lane < L) tile[lane][h] = x;
+  }
+  __syncthreads();
+  for (int i = tid; i < n_el; i += kTh) out[i] = tile[i / H][i % H];
+}
+
 // ---------------------------------------------------------------------------
 // Scaled K K^T: A = strict_tril(b_i (k_i . k_j) exp(gc_i - gc_j)).  One wave per
 // (chunk, head); the four waves of a block take four heads.
@@ -820,6 +918,18 @@ extern "C" int xk_chunk_local_cumsum(const void* g, xk_dtype g_dtype, float* out
   p.H = static_cast<int>(H);
   p.chunk = static_cast<int>(chunk_size);
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (chunk_size == kC && H <= kTileMaxHeads && N <= kScanLdsSeqs) {
+    // One block per chunk (at most T / 64 + N), then the tiles of tokens
+    // outside every sequence (at most T / 64 + 2 more, less the chunks).
+    const int64_t blocks = cdiv(total_tokens, kC) + N + 2;
+    switch (g_dtype) {
+      case XK_F32: hipLaunchKernelGGL(chunk_cumsum_tile_kernel<float>, dim3(blocks), dim3(kTh), 0, s, p); break;
+      case XK_BF16: hipLaunchKernelGGL(chunk_cumsum_tile_kernel<bf16>, dim3(blocks), dim3(kTh), 0, s, p); break;
+      case XK_F16: hipLaunchKernelGGL(chunk_cumsum_tile_kernel<f16>, dim3(blocks), dim3(kTh), 0, s, p); break;
+      default: return XK_ERR_UNSUPPORTED;
+    }
+    return launch_status();
+  }
   if (chunk_size <= kC) {
     const int64_t blocks = cdiv(cdiv(total_tokens, kWave) * H, kTh / kWave);
     switch (g_dtype) {
