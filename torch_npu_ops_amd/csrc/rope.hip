@@ -181,7 +181,7 @@ __global__ void __launch_bounds__(1024) split_rmsnorm_rope_kernel(RopeParams p) 
 #pragma unroll
     for (int u = 0; u < kVec; ++u) ss = fmaf(x1[u], x1[u], fmaf(x2[u], x2[u], ss));
     ss = group_sum<kTeam>(ss);
-    const float r = 1.0f / sqrtf(ss * (1.0f / HD) + p.eps);
+    const float r = rsqrt_hw(ss * (1.0f / HD) + p.eps);
     float o1[kVec], o2[kVec];
 #pragma unroll
     for (int u = 0; u < kVec; ++u) {
@@ -281,7 +281,7 @@ __global__ void __launch_bounds__(256) split_rmsnorm_rope_tok_kernel(RopeParams 
 #pragma unroll
     for (int u = 0; u < kVec; ++u) ss = fmaf(x1[u], x1[u], fmaf(x2[u], x2[u], ss));
     ss = group_sum<kTeam>(ss);
-    const float r = 1.0f / sqrtf(ss * (1.0f / HD) + p.eps);
+    const float r = rsqrt_hw(ss * (1.0f / HD) + p.eps);
     const float bs = is_q ? qbs : kbs;
     float o1[kVec], o2[kVec];
 #pragma unroll

@@ -121,6 +121,12 @@ __device__ __forceinline__ float fast_rcp(float x) {
   return __builtin_amdgcn_rcpf(x);
 }
 
+// Hardware reciprocal square root (v_rsq_f32, within ~1 ulp), for norm
+// scales of positive arguments (a sum of squares plus eps): one instruction
+// where 1.0f / sqrtf(x) is an IEEE square root and an IEEE division
+// sequence.
+__device__ __forceinline__ float rsqrt_hw(float x) { return __builtin_amdgcn_rsqf(x); }
+
 __device__ __forceinline__ float sigmoid(float x) {
   return fast_rcp(1.0f + __expf(-x));
 }
