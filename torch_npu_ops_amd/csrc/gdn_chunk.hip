@@ -102,6 +102,17 @@ __device__ __forceinline__ char* rec_at(const ChunkParams& p, int64_t c, int hv)
   return p.rec + (c * p.HV + hv) * static_cast<int64_t>(kRec);
 }
 
+// v-head of head slot c (item % HV) of the state kernels, whose blocks run
+// on XCD c % 8.  With H a multiple of 8 the G = HV / H v-heads of one
+// qk-head get slots of one XCD, so that their q / k reads meet in that
+// XCD's L2 (at config 4 on MI355X the state kernel then reads q and k from
+// HBM once instead of twice: 583 -> 451 MB fetched per call).
+__device__ __forceinline__ int state_head(int c, int HV, int H) {
+  if (H % 8 != 0) return c;
+  const int G = HV / H, x = c & 7, q = c >> 3;
+  return G * (x + 8 * (q / G)) + q % G;
+}
+
 // Rows >= L of the K / Q operands (q4_load) repeat row L-1; here every
 // consumer zeroes them through factors that are 0 there (beta, ck, ed, the
 // masks of M and Aq).
@@ -427,7 +438,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   const int64_t item = (r / nvt) * 8 + xcd;  // (sequence rank, head) index
   if (item >= p.N * p.HV) return;            // whole block
   const int64_t n = p.seq_order[item / p.HV];
-  const int hv = static_cast<int>(item % p.HV);
+  const int hv = state_head(static_cast<int>(item % p.HV), p.HV, p.H);
   const int hq = hv / (p.HV / p.H);
   const int V = nvt * BV;
   const int v0 = vt * BV;
@@ -674,14 +685,30 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 // ---------------------------------------------------------------------------
 constexpr int kTh8 = 512;
 
+// The transposed tiles below have unpadded rows, 16-byte chunk c of row r
+// stored at chunk c ^ (r & 15) (state copy: 128 keys, 16 chunks a row) or
+// c ^ (r & 7) (64-token tiles, 8 chunks a row).  Their MFMA operand reads
+// (ds_read_b128 of one chunk from 16 consecutive rows) then touch 16
+// distinct chunks of each 256-byte bank line, which a probe on MI355X
+// measured free of bank conflicts; padded rows of 272 / 144 bytes cost an
+// extra cycle per 16 lanes.  The 8-byte stores of MFMA results keep one
+// extra cycle per 16 lanes either way (stores take 128 bytes a cycle, and
+// the 16 rows' half-chunks have one parity).
+__device__ __forceinline__ int sb8_off(int r, int c) {
+  return r * 128 + (((c >> 3) ^ (r & 15)) << 3) + (c & 7);
+}
+__device__ __forceinline__ int t8_off(int r, int c) {
+  return r * 64 + (((c >> 3) ^ (r & 7)) << 3) + (c & 7);
+}
+
 template <int K>
 struct __align__(16) P2Smem8 {
-  __bf16 sb[2][64][K + 8];  // state hi / lo, transposed: sb[h][v][k]
+  __bf16 sb[2][64 * K];     // state hi / lo, transposed: [v][k] (sb8_off)
   __bf16 kr[2][kC * K];     // chunk key rows (kr_off layout), double-buffered
   __bf16 qr[kC * K];        // chunk query rows (kr_off layout)
-  __bf16 rt[2][64][kLt];    // R transposed, hi / lo
-  __bf16 vt[64][kLt];       // Vn transposed (bf16, for the output)
-  __bf16 dt[2][64][kLt];    // (ed * Vn) transposed, hi / lo
+  __bf16 rt[2][64 * kC];    // R transposed, hi / lo (t8_off)
+  __bf16 vt[64 * kC];       // Vn transposed (bf16, for the output)
+  __bf16 dt[2][64 * kC];    // (ed * Vn) transposed, hi / lo
   float fac[2][4 * kC];     // per-token factors cq, ck, beta, ed of the chunk, double-buffered
 };
 
@@ -709,7 +736,11 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
   constexpr int NJ = 2;  // 16-column tiles per wave
   const int tid = threadIdx.x;
   const int wid = wave_index();
-  const int wr = wid & 3, cg = wid >> 2, cb = 32 * cg;
+  // Waves w and w + 4 share a SIMD; they take token rows wr and 3 - wr, so
+  // that every SIMD gets the same share of the triangular products (Ai and
+  // Aq hold 1, 1, 2, 2 nonzero 32-wide pieces for rows 0..3).  Measured on
+  // MI355X at config 4: 283.0 -> 280.1 us per call.
+  const int cg = wid >> 2, wr = cg ? 3 - (wid & 3) : (wid & 3), cb = 32 * cg;
   const int lane = tid & 63;
   const int l15 = lane & 15, lg = lane >> 4;
   const int rl = lane >> 4, ch = lane & 15;  // whole-row loads: row in a load, 16-byte chunk
@@ -719,7 +750,7 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
   const int64_t item = (r / nvt) * 8 + xcd;
   if (item >= p.N * p.HV) return;
   const int64_t n = p.seq_order[item / p.HV];
-  const int hv = static_cast<int>(item % p.HV);
+  const int hv = state_head(static_cast<int>(item % p.HV), p.HV, p.H);
   const int hq = hv / (p.HV / p.H);
   const int V = nvt * BV;
   const int v0 = vt * BV;
@@ -747,8 +778,8 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
         Vec<__bf16, 4> h, l;
         split4(sreg[m2][nj], h, l);
         const int k0 = wr * (K / 4) + m2 * 16 + 4 * lg;
-        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][cb + nj * 16 + l15][k0]) = h;
-        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[1][cb + nj * 16 + l15][k0]) = l;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][sb8_off(cb + nj * 16 + l15, k0)]) = h;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[1][sb8_off(cb + nj * 16 + l15, k0)]) = l;
       }
   };
   publish_state();
@@ -839,8 +870,8 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
       const bf8_t ka = kr_a(kr, wr, kk);
 #pragma unroll
       for (int nj = 0; nj < NJ; ++nj) {
-        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][cb + nj * 16 + l15][kk * 32 + 8 * lg]);
-        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][cb + nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][sb8_off(cb + nj * 16 + l15, kk * 32 + 8 * lg)]);
+        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][sb8_off(cb + nj * 16 + l15, kk * 32 + 8 * lg)]);
         ks[nj] = mfma16(ka, sh, ks[nj]);
         ks[nj] = mfma16(ka, sl, ks[nj]);
       }
@@ -853,8 +884,8 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) rv[i] = bt[i] * vc[i] - ck[i] * ks[nj][i];
       split4(rv, h, l);
-      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[0][cb + nj * 16 + l15][wr * 16 + 4 * lg]) = h;
-      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[1][cb + nj * 16 + l15][wr * 16 + 4 * lg]) = l;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[0][t8_off(cb + nj * 16 + l15, wr * 16 + 4 * lg)]) = h;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.rt[1][t8_off(cb + nj * 16 + l15, wr * 16 + 4 * lg)]) = l;
     }
     __syncthreads();  // (1)
 
@@ -866,8 +897,8 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         if (kk * 32 > wr * 16 + 15) continue;
-        const bf8_t rh = *reinterpret_cast<const bf8_t*>(&sm.rt[0][cb + nj * 16 + l15][kk * 32 + 8 * lg]);
-        const bf8_t rl2 = *reinterpret_cast<const bf8_t*>(&sm.rt[1][cb + nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t rh = *reinterpret_cast<const bf8_t*>(&sm.rt[0][t8_off(cb + nj * 16 + l15, kk * 32 + 8 * lg)]);
+        const bf8_t rl2 = *reinterpret_cast<const bf8_t*>(&sm.rt[1][t8_off(cb + nj * 16 + l15, kk * 32 + 8 * lg)]);
         vn[nj] = mfma_split3(inv.aiH[kk], inv.aiL[kk], rh, rl2, vn[nj]);
       }
     }
@@ -881,9 +912,9 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
         d[i] = ed[i] * vn[nj][i];
       }
       split4(d, h, l);
-      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.vt[cb + nj * 16 + l15][wr * 16 + 4 * lg]) = b;
-      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][cb + nj * 16 + l15][wr * 16 + 4 * lg]) = h;
-      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[1][cb + nj * 16 + l15][wr * 16 + 4 * lg]) = l;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.vt[t8_off(cb + nj * 16 + l15, wr * 16 + 4 * lg)]) = b;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[0][t8_off(cb + nj * 16 + l15, wr * 16 + 4 * lg)]) = h;
+      *reinterpret_cast<Vec<__bf16, 4>*>(&sm.dt[1][t8_off(cb + nj * 16 + l15, wr * 16 + 4 * lg)]) = l;
     }
     load_inv8(inv, cidx0 + cn);
     // (Q S)^T = S^T Q^T: Q's rows from the query tile, keys in natural order.
@@ -895,7 +926,7 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
       const bf8_t qa = kr_a(sm.qr, wr, kk);
 #pragma unroll
       for (int nj = 0; nj < NJ; ++nj) {
-        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][cb + nj * 16 + l15][kk * 32 + 8 * lg]);
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][sb8_off(cb + nj * 16 + l15, kk * 32 + 8 * lg)]);
         qs[nj] = mfma16(sh, qa, qs[nj]);
       }
     }
@@ -914,7 +945,7 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           if (kk * 32 > wr * 16 + 15) continue;
-          const bf8_t vb = *reinterpret_cast<const bf8_t*>(&sm.vt[cb + nj * 16 + l15][kk * 32 + 8 * lg]);
+          const bf8_t vb = *reinterpret_cast<const bf8_t*>(&sm.vt[t8_off(cb + nj * 16 + l15, kk * 32 + 8 * lg)]);
           acc = mfma16(vb, outo.aq[kk], acc);
         }
         Vec<bf16, 4> ov;
@@ -939,8 +970,8 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
         for (int i = 0; i < 4; ++i) acc[i] *= cur.egl;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const bf8_t dh = *reinterpret_cast<const bf8_t*>(&sm.dt[0][cb + nj * 16 + l15][kk * 32 + 8 * lg]);
-          const bf8_t dl = *reinterpret_cast<const bf8_t*>(&sm.dt[1][cb + nj * 16 + l15][kk * 32 + 8 * lg]);
+          const bf8_t dh = *reinterpret_cast<const bf8_t*>(&sm.dt[0][t8_off(cb + nj * 16 + l15, kk * 32 + 8 * lg)]);
+          const bf8_t dl = *reinterpret_cast<const bf8_t*>(&sm.dt[1][t8_off(cb + nj * 16 + l15, kk * 32 + 8 * lg)]);
           acc = mfma16(ka[kk], dh, acc);
           acc = mfma16(ka[kk], dl, acc);
         }
