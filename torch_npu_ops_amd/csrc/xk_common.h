@@ -105,11 +105,36 @@ __device__ __forceinline__ void store_vec_f32(T* p, const float (&in)[N]) {
 // ---------------------------------------------------------------------------
 // Reductions.
 // ---------------------------------------------------------------------------
-// Sum over aligned groups of `width` lanes (width a power of two <= 64).
+// One DPP move of a float (every row and bank enabled).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Lane l's value, broadcast (v_readlane).
+__device__ __forceinline__ float readlane_f32(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64),
+// every lane of a group receiving the sum; every lane of a group must be
+// active.  Within a 16-lane row the butterfly runs on DPP moves (quad
+// permutations, then the half-row and row mirrors), a few cycles each where
+// a ds_bpermute shuffle is an LDS round trip; rows combine through
+// v_readlane.
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  static_assert(WIDTH >= 1 && WIDTH <= 64 && (WIDTH & (WIDTH - 1)) == 0, "power of two <= 64");
+  if constexpr (WIDTH >= 2) v += dpp_f32<0xB1>(v);   // quad_perm(1,0,3,2): lane ^ 1
+  if constexpr (WIDTH >= 4) v += dpp_f32<0x4E>(v);   // quad_perm(2,3,0,1): lane ^ 2
+  if constexpr (WIDTH >= 8) v += dpp_f32<0x141>(v);  // row_half_mirror: quad pairs
+  if constexpr (WIDTH >= 16) v += dpp_f32<0x140>(v); // row_mirror: half-row pairs
+  if constexpr (WIDTH >= 32) {
+    const float a = readlane_f32(v, 0) + readlane_f32(v, 16);
+    const float b = readlane_f32(v, 32) + readlane_f32(v, 48);
+    v = WIDTH == 64 ? a + b : ((threadIdx.x & 32) ? b : a);
+  }
   return v;
 }
 
