@@ -36,6 +36,7 @@ struct Seq {
   int64_t N;
   int64_t T;  // token rows
   int32_t* chunk_off;
+  int32_t* seq_order;  // sequences, longest first (fwd_h), or NULL
   int64_t NTmax;
 };
 
@@ -523,7 +524,9 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
   const int vt = static_cast<int>(r % p.nvt);
   const int64_t item = (r / p.nvt) * 8 + (bid & 7);  // same XCD for one (n, h)
   if (item >= p.N * p.H) return;
-  const int64_t n = item / p.H;
+  // Items are dispatched longest sequence first: the longest chains start in
+  // the first wave of resident blocks and shorter ones fill in behind them.
+  const int64_t n = p.seq_order[item / p.H];
   const int h = static_cast<int>(item % p.H);
   const int hq = h / (p.H / p.Hg);
   const int V = p.nvt * kBV, v0 = vt * kBV;
@@ -877,18 +880,23 @@ int seq_init(Seq& q, const void* cu, xk_dtype cu_dtype, int64_t N, int64_t T, vo
   q.T = T;
   q.NTmax = T / kC + N;
   q.chunk_off = nullptr;
+  q.seq_order = nullptr;
   if (need_offsets) {
-    if (!ws || static_cast<int64_t>(ws_bytes) < align256(4 * (N + 1)) || !aligned(ws, 256))
+    if (!ws || static_cast<int64_t>(ws_bytes) < align256(4 * (N + 1)) + align256(4 * N) ||
+        !aligned(ws, 256))
       return XK_ERR_WORKSPACE;
     q.chunk_off = static_cast<int32_t*>(ws);
+    q.seq_order = reinterpret_cast<int32_t*>(static_cast<char*>(ws) + align256(4 * (N + 1)));
   }
   return XK_OK;
 }
 
+// Chunk offsets, and with `order` the longest-first ranking of the
+// sequences into p.seq_order.
 template <class P>
-int launch_offsets(const P& p, hipStream_t s) {
-  hipLaunchKernelGGL(chunk_offsets_kernel<P>, dim3(1), dim3(256), 0, s, p, nullptr, nullptr,
-                     int64_t{0});
+int launch_offsets(const P& p, hipStream_t s, bool order = false) {
+  hipLaunchKernelGGL(chunk_offsets_kernel<P>, dim3(1), dim3(256), 0, s, p,
+                     order ? p.seq_order : nullptr, nullptr, int64_t{0});
   return launch_status();
 }
 
@@ -900,7 +908,7 @@ using namespace xk::gdn;
 
 extern "C" int64_t xk_gdn_stage_workspace_bytes(int64_t num_seqs) {
   if (num_seqs < 0) return -1;
-  return align256(4 * (num_seqs + 1));
+  return align256(4 * (num_seqs + 1)) + align256(4 * num_seqs);
 }
 
 extern "C" int xk_chunk_local_cumsum(const void* g, xk_dtype g_dtype, float* out,
@@ -1071,7 +1079,7 @@ extern "C" int xk_chunk_fwd_h(const void* k, const void* w, const void* u, xk_dt
   p.Hg = static_cast<int>(Hg);
   p.nvt = static_cast<int>(V / kBV);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if ((st = launch_offsets(p, s))) return st;
+  if ((st = launch_offsets(p, s, true))) return st;
   const int64_t blocks = cdiv(N * H, 8) * 8 * p.nvt;
   hipLaunchKernelGGL(chunk_fwd_h_kernel<128>, dim3(blocks), dim3(kTh), 0, s, p);
   return launch_status();
