@@ -1727,6 +1727,11 @@ def main():
             del c
         cpu = ops[headline].get("cpu_baseline")
     traffic = measured_traffic(case)
+    # Every op's dominant kernel carries its counted HBM bytes per dispatch
+    # too (null, with a warning, when its source changed since the counters
+    # were taken).
+    for name in names:
+        ops[name]["roofline"]["traffic"] = measured_traffic(CASES[name])
     line = {
         "metric": "achieved HBM GB/s (% of peak) per op; chunked GDN prefill tokens/s",
         "value": head["GB/s"],
