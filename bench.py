@@ -921,7 +921,7 @@ class GdnChunkStagedCase(GdnChunkCase):
               "scaled_dot_kkt, solve_tril, recompute_w_u, fwd_h, fwd_o), the "
               "reference's intermediates (A, Ai, w, u, h, v_new) kept in HBM")
     source = "gdn_stages.hip"
-    kernel = "chunk_fwd_h_kernel"
+    kernel = "chunk_fwd_h8_kernel"
 
     def nchunks(self):
         lens = (self.cu[1:] - self.cu[:-1]).tolist()
@@ -950,7 +950,7 @@ class GdnChunkStagedCase(GdnChunkCase):
             ("solve_tril", "solve_tril_kernel", A_b + Ai_b + cu),
             ("recompute_w_u", "recompute_w_u_kernel",
              k_b + v_b + bt_b + g_b + Ai_b + w_b + v_b + cu),
-            ("chunk_fwd_h", "chunk_fwd_h_kernel", k_b + w_b + v_b + g_b + 2 * s_b + h_b + v_b + cu),
+            ("chunk_fwd_h", "chunk_fwd_h8_kernel", k_b + w_b + v_b + g_b + 2 * s_b + h_b + v_b + cu),
             ("chunk_fwd_o", "chunk_fwd_o_kernel", 2 * k_b + v_b + h_b + g_b + v_b + cu),
         ]
 

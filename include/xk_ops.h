@@ -420,7 +420,7 @@ int xk_solve_tril(const float* A, void* Ai, xk_dtype ai_dtype,
                   size_t workspace_bytes, void* stream);
 
 /* u = Ai (v beta), w = Ai (k beta exp(gc)); Ai bf16 or fp32, outputs bf16.
- * Replaces npu_recompute_w_u_fwd (triton_ops_api.h:51-57,
+ * k, v, Ai, w and u 16-byte aligned (else XK_ERR_INVALID).  Replaces npu_recompute_w_u_fwd (triton_ops_api.h:51-57,
  * npu_triton_chunk_gated_delta_rule.cpp:397-475). */
 int xk_recompute_w_u(const void* k, const void* v, xk_dtype dtype,
                      const void* beta, xk_dtype beta_dtype,

@@ -102,17 +102,6 @@ __device__ __forceinline__ char* rec_at(const ChunkParams& p, int64_t c, int hv)
   return p.rec + (c * p.HV + hv) * static_cast<int64_t>(kRec);
 }
 
-// v-head of head slot c (item % HV) of the state kernels, whose blocks run
-// on XCD c % 8.  With H a multiple of 8 the G = HV / H v-heads of one
-// qk-head get slots of one XCD, so that their q / k reads meet in that
-// XCD's L2 (at config 4 on MI355X the state kernel then reads q and k from
-// HBM once instead of twice: 583 -> 451 MB fetched per call).
-__device__ __forceinline__ int state_head(int c, int HV, int H) {
-  if (H % 8 != 0) return c;
-  const int G = HV / H, x = c & 7, q = c >> 3;
-  return G * (x + 8 * (q / G)) + q % G;
-}
-
 // Rows >= L of the K / Q operands (q4_load) repeat row L-1; here every
 // consumer zeroes them through factors that are 0 there (beta, ck, ed, the
 // masks of M and Aq).
@@ -159,8 +148,11 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int l15 = lane & 15, lg = lane >> 4;
-  const int64_t c = blockIdx.x;
-  const int hv = blockIdx.y * 4 + wid;
+  // Blocks take the head groups of one chunk before the next chunk, so
+  // that the blocks in flight read whole token rows.
+  const int hg4 = (p.HV + 3) >> 2;
+  const int64_t c = blockIdx.x / hg4;
+  const int hv = static_cast<int>(blockIdx.x % hg4) * 4 + wid;
   const int2 ce = p.ctab[c];  // (first token, length); length 0 past the last chunk
   const int64_t s = ce.x;
   const int L = ce.y;
@@ -685,21 +677,7 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
 // ---------------------------------------------------------------------------
 constexpr int kTh8 = 512;
 
-// The transposed tiles below have unpadded rows, 16-byte chunk c of row r
-// stored at chunk c ^ (r & 15) (state copy: 128 keys, 16 chunks a row) or
-// c ^ (r & 7) (64-token tiles, 8 chunks a row).  Their MFMA operand reads
-// (ds_read_b128 of one chunk from 16 consecutive rows) then touch 16
-// distinct chunks of each 256-byte bank line, which a probe on MI355X
-// measured free of bank conflicts; padded rows of 272 / 144 bytes cost an
-// extra cycle per 16 lanes.  The 8-byte stores of MFMA results keep one
-// extra cycle per 16 lanes either way (stores take 128 bytes a cycle, and
-// the 16 rows' half-chunks have one parity).
-__device__ __forceinline__ int sb8_off(int r, int c) {
-  return r * 128 + (((c >> 3) ^ (r & 15)) << 3) + (c & 7);
-}
-__device__ __forceinline__ int t8_off(int r, int c) {
-  return r * 64 + (((c >> 3) ^ (r & 7)) << 3) + (c & 7);
-}
+// The transposed tiles below (sb8_off, t8_off) are unpadded and swizzled.
 
 template <int K>
 struct __align__(16) P2Smem8 {
@@ -1007,7 +985,9 @@ int launch_chunk(const ChunkParams& p, int64_t V, hipStream_t s) {
                      p.seq_order, p.ctab, p.NTmax);
   int st = launch_status();
   if (st) return st;
-  hipLaunchKernelGGL((gdn_chunk_prep_kernel<K, GT, BT>), dim3(p.NTmax, (p.HV + 3) / 4),
+  const int64_t prep_blocks = p.NTmax * ((p.HV + 3) / 4);
+  if (prep_blocks > INT32_MAX) return XK_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((gdn_chunk_prep_kernel<K, GT, BT>), dim3(static_cast<uint32_t>(prep_blocks)),
                      dim3(kTh), 0, s, p);
   st = launch_status();
   if (st) return st;

@@ -269,6 +269,76 @@ __device__ __forceinline__ bf8_t kr_at(const __bf16* kr, int mi, int kk) {
   return cat_bf8(kr_col4(kr, mi, r0), kr_col4(kr, mi, r0 + 4));
 }
 
+// Transposed tiles of the state kernels have unpadded rows, 16-byte chunk c of row r
+// stored at chunk c ^ (r & 15) (state copy: 128 keys, 16 chunks a row) or
+// c ^ (r & 7) (64-token tiles, 8 chunks a row).  Their MFMA operand reads
+// (ds_read_b128 of one chunk from 16 consecutive rows) then touch 16
+// distinct chunks of each 256-byte bank line, which a probe on MI355X
+// measured free of bank conflicts; padded rows of 272 / 144 bytes cost an
+// extra cycle per 16 lanes.  The 8-byte stores of MFMA results keep one
+// extra cycle per 16 lanes either way (stores take 128 bytes a cycle, and
+// the 16 rows' half-chunks have one parity).
+__device__ __forceinline__ int sb8_off(int r, int c) {
+  return r * 128 + (((c >> 3) ^ (r & 15)) << 3) + (c & 7);
+}
+__device__ __forceinline__ int t8_off(int r, int c) {
+  return r * 64 + (((c >> 3) ^ (r & 7)) << 3) + (c & 7);
+}
+
+// Column c0 + lane % 16 of a 64-wide t8_off tile at rows r0 .. r0 + 3 (c0 a
+// multiple of 16 shared by a 16-lane group, r0 per group), as kr_col4.
+__device__ __forceinline__ s4_t t8_col4(const __bf16* t, int c0, int r0) {
+  typedef __attribute__((address_space(3))) s4_t lds_s4;
+  const int s = threadIdx.x & 15;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(t + t8_off(r0 + (s >> 2), c0 + 4 * (s & 3))));
+}
+// Column c0 + lane % 16 of a 128-wide sb8_off tile at rows r0 .. r0 + 3.
+__device__ __forceinline__ s4_t sb8_col4(const __bf16* t, int c0, int r0) {
+  typedef __attribute__((address_space(3))) s4_t lds_s4;
+  const int s = threadIdx.x & 15;
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(t + sb8_off(r0 + (s >> 2), c0 + 4 * (s & 3))));
+}
+
+// v-head of head slot c (item % HV) of the state kernels, whose blocks run
+// on XCD c % 8.  With H a multiple of 8 the G = HV / H v-heads of one
+// qk-head get slots of one XCD, so that their q / k reads meet in that
+// XCD's L2 (at config 4 on MI355X the state kernel then reads q and k from
+// HBM once instead of twice: 583 -> 451 MB fetched per call).
+__device__ __forceinline__ int state_head(int c, int HV, int H) {
+  if (H % 8 != 0) return c;
+  const int G = HV / H, x = c & 7, q = c >> 3;
+  return G * (x + 8 * (q / G)) + q % G;
+}
+
+// kr_at with the columns paired for 16-byte stores: lane (g, j) gets column
+// 32 a + 8 (j / 4) + 4 hb + j % 4 at rows 32 kk + 8 g .. + 7 (each 16-lane
+// group of a transposed read may address any four 4-column groups).  The C
+// tiles of hb = 0 and 1 then give lane (g, j) columns 32 a + 8 g .. + 7 of
+// row j of the product.
+__device__ __forceinline__ bf8_t kr_at_pair(const __bf16* kr, int a, int hb, int kk) {
+  typedef __attribute__((address_space(3))) s4_t lds_s4;
+  const int lane = threadIdx.x & 63, s = lane & 15;
+  const int r0 = 32 * kk + 8 * (lane >> 4) + (s >> 2);
+  const __bf16* p0 = kr + kr_off(r0, 4 * a + (s & 3)) + 4 * hb;
+  const __bf16* p1 = kr + kr_off(r0 + 4, 4 * a + (s & 3)) + 4 * hb;
+  return cat_bf8(__builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p0)),
+                 __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p1)));
+}
+
+// Direct global -> LDS loads of 16 bytes per lane: lane l's bytes from `src`
+// land at `lds` + 16 l (`lds` wave-uniform).  They count in vmcnt, and a
+// workgroup barrier alone does not wait for them, so dma_sync waits for
+// every outstanding load first (as the builtin, so that the compiler knows
+// they are complete and adds no wait of its own later).
+typedef __attribute__((address_space(3))) void lds_void;
+__device__ __forceinline__ void dma16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
+}
+__device__ __forceinline__ void dma_sync() {
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt, expcnt and lgkmcnt all 0
+  __syncthreads();
+}
+
 // kr_at with the rows in q4_to_a's key order: rows q4_key(kk, lane / 16)
 // .. + 7, the partner of an operand kk that went through q4_to_a.
 __device__ __forceinline__ bf8_t kr_at_q4(const __bf16* kr, int mi, int kk) {

@@ -244,10 +244,13 @@ __global__ void __launch_bounds__(kTh) chunk_kkt_kernel(KktParams p) {
   // the DPP transposes (q4_to_a) run with every lane of the wave active.
   const int wid = wave_index(), lane = threadIdx.x & 63;
   const int l15 = lane & 15, lg = lane >> 4;
-  const int h = blockIdx.y * 4 + wid;
+  // Blocks take the head groups of one chunk before the next chunk, so
+  // that the blocks in flight read whole token rows.
+  const int hg4 = (p.H + 3) >> 2;
+  const int h = static_cast<int>(blockIdx.x % hg4) * 4 + wid;
   int64_t n, s;
   int L;
-  if (!(h < p.H && locate_chunk(p, blockIdx.x, n, s, L))) return;  // wave-uniform
+  if (!(h < p.H && locate_chunk(p, blockIdx.x / hg4, n, s, L))) return;  // wave-uniform
   const int hq = h / (p.H / p.Hg);
   constexpr int KK = K / 32;
   // Key rows loaded quad-contiguously (q4_load; rows >= L repeat row L-1)
@@ -310,10 +313,13 @@ template <typename OT>
 __global__ void __launch_bounds__(kTh) solve_tril_kernel(TrilParams p) {
   __shared__ __align__(16) float lds[4][kC][kLd];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int h = blockIdx.y * 4 + wid;
+  // Blocks take the head groups of one chunk before the next chunk, so
+  // that the blocks in flight read whole token rows.
+  const int hg4 = (p.H + 3) >> 2;
+  const int h = static_cast<int>(blockIdx.x % hg4) * 4 + wid;
   int64_t n, s;
   int L;
-  if (!(h < p.H && locate_chunk(p, blockIdx.x, n, s, L))) return;  // wave-uniform
+  if (!(h < p.H && locate_chunk(p, blockIdx.x / hg4, n, s, L))) return;  // wave-uniform
   float (*X)[kLd] = lds[wid];
   // Access j covers rows 8j .. 8j + 7 (lane: row 8j + lane / 8, columns
   // 8 (lane % 8) .. + 7), so every instruction moves whole rows.  Strictly
@@ -349,9 +355,7 @@ __global__ void __launch_bounds__(kTh) solve_tril_kernel(TrilParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// WY recompute: u = Ai (v b), w = Ai (k b exp(gc)).  One block per (chunk, head); the
-// right-hand side is staged transposed (token-contiguous) as bf16 hi / lo,
-// wave w produces output columns [w*D/4, (w+1)*D/4) of all 64 rows.
+// WY recompute: u = Ai (v b), w = Ai (k b exp(gc)).
 // ---------------------------------------------------------------------------
 struct WuParams : Seq {
   const void* k;
@@ -367,107 +371,106 @@ struct WuParams : Seq {
 constexpr int kLt = kC + 8;  // bf16 LDS row stride (144 B: 16-byte aligned)
 
 // One block per (chunk, head); wave w owns tokens 16w .. 16w + 15 of both
-// products.  Each product is formed transposed, out^T = rhs^T Ai^T, so a
-// lane owns one token and 4 consecutive columns of it (8-byte stores), and
-// the wave's Ai rows are the B operands of both products (loaded once).
-// The right-hand sides (v beta and k beta exp(gc), fp32) reach LDS
-// transposed as hi / lo bf16: the wave's 16 token rows go through
-// select_op MFMAs (exact), are scaled per token in the MFMA C layout and
-// split there, and leave as 8-byte vectors.  Ai is lower triangular, so
+// products.  The per-token factors are folded into Ai's columns,
+// u = (Ai diag(b)) v and w = (Ai diag(b exp(gc))) k, so the right-hand
+// sides are the raw bf16 rows: they go from HBM straight into LDS tiles by
+// direct loads (no registers, no conversion), while each lane loads its
+// Ai row, and the block waits once for all of it.  The scaled Ai rows are
+// split hi / lo in registers (fp32 to ~2^-16) and are the B operands of both
+// products, formed transposed, out^T = rhs^T Ai'^T, so that a lane owns one
+// token and (through kr_at_pair's column order) 8 consecutive columns of it:
+// 16-byte stores.  Factors of key tokens >= L are 0, so those rows of the
+// tiles (copies of row L - 1) add nothing.  Ai is lower triangular, so
 // waves 0 and 1 skip the key tokens 32 .. 63.
-
 template <typename BT, typename AT>
 __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
   constexpr int D = 128;  // K = V = 128
-  __shared__ __align__(16) __bf16 bt[2][kC * D];  // rhs rows hi / lo (kr_off layout)
-  __shared__ float fb[kC], fk[kC];
-  const int h = blockIdx.y;
+  static_assert(D == kKrRow, "row tiles of 128 bf16");
+  __shared__ __align__(16) __bf16 vt[kC * D];  // v rows (kr_off layout)
+  __shared__ __align__(16) __bf16 kt[kC * D];  // k rows (kr_off layout)
+  __shared__ __align__(16) float fb[kC], fk[kC];
+  // Blocks take the heads of one chunk before the next chunk, so that the
+  // blocks in flight read whole token rows.
+  const int h = static_cast<int>(blockIdx.x % p.H);
   int64_t n, s;
   int L;
-  if (!locate_chunk(p, blockIdx.x, n, s, L)) return;  // block-uniform
+  if (!locate_chunk(p, blockIdx.x / p.H, n, s, L)) return;  // block-uniform
   const int hq = h / (p.H / p.Hg);
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int l15 = lane & 15, lg = lane >> 4;
-  if (threadIdx.x < kC) {
-    const int t = min(static_cast<int>(threadIdx.x), L - 1);
-    const float b = ldf<BT>(p.beta, (s + t) * p.H + h);
-    fb[threadIdx.x] = b;
-    fk[threadIdx.x] = b * __expf(p.gcum ? p.gcum[(s + t) * p.H + h] : 0.f);
+  // Rows 16w + 4j + lane / 16 of both tiles, 1 KB per load; LDS chunk
+  // lane % 16 of row r holds the row's chunk (lane % 16) ^ (r % 16).
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = wid * 16 + 4 * j + lg;
+    const int64_t t = s + min(r, L - 1);
+    const int c = l15 ^ (r & 15);
+    dma16(reinterpret_cast<const bf16*>(p.v) + (t * p.H + h) * D + 8 * c, vt + (wid * 16 + 4 * j) * D);
+    dma16(reinterpret_cast<const bf16*>(p.k) + (t * p.Hg + hq) * D + 8 * c, kt + (wid * 16 + 4 * j) * D);
   }
-  const int tq = wid * 16 + l15;  // this lane's token
-  // Ai row tq (B operands), hi / lo for fp32 Ai.
+  // Ai row tq, keys 32 kk + 8 lg .. + 7 (B operand layout).
+  const int tq = wid * 16 + l15;
   const AT* arow = reinterpret_cast<const AT*>(p.Ai) + ((s + min(tq, L - 1)) * p.H + h) * kC + 8 * lg;
-  bf8_t aih[2], ail[2];
+  float ai[2][8];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) load_vec_f32<AT, 8>(arow + 32 * kk, ai[kk]);
+  // The 64 token factors (lane = token), loaded last so that their wait
+  // overlaps the loads above.
+  const int64_t ft = (s + min(lane, L - 1)) * p.H + h;
+  const float bval = ldf<BT>(p.beta, ft);
+  const float gval = p.gcum ? p.gcum[ft] : 0.f;
+  if (wid == 0) {
+    fb[lane] = lane < L ? bval : 0.f;
+    fk[lane] = lane < L ? bval * __expf(gval) : 0.f;
+  }
+  dma_sync();  // tiles, Ai rows and factors
+
+  bf8_t uh[2], ul[2], wh[2], wl[2];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
-    if constexpr (std::is_same<AT, float>::value) {
-      split8(arow + kk * 32, aih[kk], ail[kk]);
-    } else {
+    const float* pb = fb + 32 * kk + 8 * lg;
+    const float* pk = fk + 32 * kk + 8 * lg;
+    alignas(16) float xb[8];
+    alignas(16) float xk[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        aih[kk][e] = static_cast<__bf16>(to_f32(arow[kk * 32 + e]));
-        ail[kk][e] = static_cast<__bf16>(0.f);
-      }
+    for (int e = 0; e < 8; ++e) {
+      xb[e] = ai[kk][e] * pb[e];
+      xk[e] = ai[kk][e] * pk[e];
     }
+    split8(xb, uh[kk], ul[kk]);
+    split8(xk, wh[kk], wl[kk]);
   }
   const f4_t zero = {0.f, 0.f, 0.f, 0.f};
-  static_assert(D == kKrRow, "row tiles of 128 bf16");
-  const int rl = lane >> 4, ch = lane & 15;  // row within a load, 16-byte chunk
-  __syncthreads();  // fb / fk
-
-#pragma unroll 1
+#pragma unroll
   for (int prod = 0; prod < 2; ++prod) {
-    // prod 0: u = Ai (v beta); prod 1: w = Ai (k beta exp(gc)).
-    // Right-hand-side rows (tokens) 16w + 4j + rl, each loaded whole by 16
-    // lanes, scaled by the token's factor (0 for rows >= L, whose loads
-    // repeat row L-1) and split hi / lo into the row tiles.
-    const float* f = prod == 0 ? fb : fk;
-    bf8_t a[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t t = s + min(wid * 16 + 4 * j + rl, L - 1);
-      const bf16* src = prod == 0 ? reinterpret_cast<const bf16*>(p.v) + (t * p.H + h) * D
-                                  : reinterpret_cast<const bf16*>(p.k) + (t * p.Hg + hq) * D;
-      a[j] = *reinterpret_cast<const bf8_t*>(src + 8 * ch);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int t = wid * 16 + 4 * j + rl;
-      const float fr = t < L ? f[t] : 0.f;
-      bf8_t xh, xl;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float x = fr * static_cast<float>(a[j][e]);
-        xh[e] = static_cast<__bf16>(x);
-        xl[e] = static_cast<__bf16>(x - static_cast<float>(xh[e]));
-      }
-      *reinterpret_cast<bf8_t*>(bt[0] + kr_off(t, ch)) = xh;
-      *reinterpret_cast<bf8_t*>(bt[1] + kr_off(t, ch)) = xl;
-    }
-    __syncthreads();  // bt complete
-
+    const __bf16* tile = prod == 0 ? vt : kt;
+    const bf8_t* bh = prod == 0 ? uh : wh;
+    const bf8_t* bl = prod == 0 ? ul : wl;
     bf16* orow = reinterpret_cast<bf16*>(prod == 0 ? p.u : p.w) +
                  ((s + min(tq, L - 1)) * p.H + h) * D;
 #pragma unroll
-    for (int nj = 0; nj < D / 16; ++nj) {
-      f4_t acc = zero;
+    for (int a = 0; a < D / 32; ++a) {
+      f4_t acc0 = zero, acc1 = zero;
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         if (kk * 32 > wid * 16 + 15) continue;  // key tokens beyond the diagonal
-        const bf8_t bh = kr_at(bt[0], nj, kk);  // rhs^T: column nj*16 + l15, tokens 32kk + 8lg ..
-        const bf8_t bl = kr_at(bt[1], nj, kk);
-        acc = mfma16(bh, aih[kk], acc);
-        acc = mfma16(bl, aih[kk], acc);
-        if constexpr (std::is_same<AT, float>::value) acc = mfma16(bh, ail[kk], acc);
+        const bf8_t r0 = kr_at_pair(tile, a, 0, kk);  // rhs^T columns, tokens 32kk + 8lg ..
+        const bf8_t r1 = kr_at_pair(tile, a, 1, kk);
+        acc0 = mfma16(r0, bh[kk], acc0);
+        acc0 = mfma16(r0, bl[kk], acc0);
+        acc1 = mfma16(r1, bh[kk], acc1);
+        acc1 = mfma16(r1, bl[kk], acc1);
       }
       if (tq < L) {
-        Vec<bf16, 4> ov;
+        Vec<bf16, 8> ov;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ov.v[i] = from_f32<bf16>(acc[i]);
-        *reinterpret_cast<Vec<bf16, 4>*>(orow + nj * 16 + 4 * lg) = ov;
+        for (int i = 0; i < 4; ++i) {
+          ov.v[i] = from_f32<bf16>(acc0[i]);
+          ov.v[4 + i] = from_f32<bf16>(acc1[i]);
+        }
+        *reinterpret_cast<Vec<bf16, 8>*>(orow + 32 * a + 8 * lg) = ov;
       }
     }
-    __syncthreads();  // bt reads done before the next product overwrites it
   }
 }
 
@@ -715,6 +718,216 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// The state recurrence for V a multiple of 64: one 512-lane block per
+// (sequence, head, 64-column V tile).  Wave (wr, cg) owns tokens 16 wr ..
+// of v_new, state key rows 32 wr .. and columns cb = 32 cg .. of the tile
+// (the fp32 state in registers, MFMA C layout).  What leaves for global
+// memory is formed so that a lane holds 8 consecutive columns of one row
+// (16-byte stores):
+//   v_new^T = u^T - S^T w^T  (A: state-copy rows, in an order that pairs
+//                             the two C tiles of a lane; B: w rows)
+//   h snapshot               (the state copy's hi part read transposed)
+// and D = v_new * decay goes to LDS as token rows, read transposed as the B
+// operand of S <- exp(gl) S + K^T D.  Two barriers per chunk.  Key and w
+// rows are loaded a chunk ahead into registers (whole rows, 16 lanes a
+// row) and written to LDS at the end of the chunk before.
+// ---------------------------------------------------------------------------
+constexpr int kTh8 = 512;
+
+template <int K>
+struct __align__(16) FwdH8Smem {
+  __bf16 sb[2][64 * K];   // state hi / lo, transposed [v][k] (sb8_off)
+  __bf16 kr[2][kC * K];   // chunk key rows (kr_off), double-buffered
+  __bf16 wt[kC * K];      // chunk w rows (kr_off)
+  __bf16 dt[2][kC * 64];  // D hi / lo, [token][v] (t8_off)
+};
+
+struct FwdH8Ops {
+  bf8_t kraw[2], wraw[2];  // key / w rows 16 wr + 8 cg + 4 j + lane / 16, chunk lane % 16
+  bf8_t ut;                // u of token 16 wr + lane % 16, columns cb + 8 (lane / 16) .. + 7
+  float gct;               // gc of that token
+  float gl;                // gc of the chunk's last token
+};
+
+template <int K>
+__global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
+  static_assert(K == 128, "key rows of 128");
+  __shared__ FwdH8Smem<K> sm;
+  constexpr int KK = K / 32, M2 = K / 64, NJ = 2;
+  const int tid = threadIdx.x, wid = wave_index(), lane = tid & 63;
+  const int l15 = lane & 15, lg = lane >> 4;
+  // Waves w and w + 4 share a SIMD and take token rows wr and 3 - wr.
+  const int cg = wid >> 2, wr = cg ? 3 - (wid & 3) : (wid & 3), cb = 32 * cg;
+  const int rl = lane >> 4, ch = lane & 15;  // whole-row loads: row in a load, 16-byte chunk
+  const int64_t bid = blockIdx.x;
+  const int64_t r = bid >> 3;
+  const int vt = static_cast<int>(r % p.nvt);
+  const int64_t item = (r / p.nvt) * 8 + (bid & 7);  // one XCD for the V tiles of (n, h)
+  if (item >= p.N * p.H) return;
+  const int64_t n = p.seq_order[item / p.H];  // longest sequences first
+  const int h = state_head(static_cast<int>(item % p.H), p.H, p.Hg);
+  const int hq = h / (p.H / p.Hg);
+  const int V = p.nvt * 64, v0 = vt * 64;
+  const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
+  const int64_t c0 = p.chunk_off[n];
+  const int64_t nch = max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.hcap - c0));
+
+  f4_t sreg[M2][NJ];
+#pragma unroll
+  for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+    for (int nj = 0; nj < NJ; ++nj)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int kr = wr * (K / 4) + m2 * 16 + 4 * lg + i;
+        sreg[m2][nj][i] = p.h0 ? p.h0[((n * p.H + h) * K + kr) * V + v0 + cb + nj * 16 + l15] : 0.f;
+      }
+  auto publish_state = [&]() {
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+      for (int nj = 0; nj < NJ; ++nj) {
+        Vec<__bf16, 4> hi, lo;
+        split4(sreg[m2][nj], hi, lo);
+        const int k0 = wr * (K / 4) + m2 * 16 + 4 * lg;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[0][sb8_off(cb + nj * 16 + l15, k0)]) = hi;
+        *reinterpret_cast<Vec<__bf16, 4>*>(&sm.sb[1][sb8_off(cb + nj * 16 + l15, k0)]) = lo;
+      }
+  };
+  const uint32_t krb = static_cast<uint32_t>(p.Hg) * K * 2;  // key row bytes
+  const uint32_t wrb = static_cast<uint32_t>(p.H) * K * 2;   // w row bytes
+  const int64_t vrow = static_cast<int64_t>(p.H) * V;         // u / v_new row elements
+  const int vcol = h * V + v0 + cb + 8 * lg;                   // this lane's u / v_new columns
+  auto load_ops = [&](FwdH8Ops& o, int64_t ci) {
+    const int64_t s = bos + ci * kC;
+    const int L = static_cast<int>(min<int64_t>(kC, eos - s));
+    const char* kb = reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.k) + (s * p.Hg + hq) * K);
+    const char* wb = reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.w) + (s * p.H + h) * K);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const uint32_t row = static_cast<uint32_t>(min(wr * 16 + cg * 8 + 4 * j + rl, L - 1));
+      o.kraw[j] = *reinterpret_cast<const bf8_t*>(kb + row * krb + 16u * ch);
+      o.wraw[j] = *reinterpret_cast<const bf8_t*>(wb + row * wrb + 16u * ch);
+    }
+    const int64_t t = s + min(wr * 16 + l15, L - 1);
+    o.ut = *reinterpret_cast<const bf8_t*>(reinterpret_cast<const bf16*>(p.u) + t * vrow + vcol);
+    o.gct = p.gcum ? p.gcum[t * p.H + h] : 0.f;
+    o.gl = p.gcum ? p.gcum[(s + L - 1) * p.H + h] : 0.f;
+  };
+  auto store_rows = [&](__bf16* tile, const bf8_t (&raw)[2]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      *reinterpret_cast<bf8_t*>(tile + kr_off(wr * 16 + cg * 8 + 4 * j + rl, ch)) = raw[j];
+  };
+
+  FwdH8Ops opsA, opsB;
+  if (nch > 0) {
+    load_ops(opsA, 0);
+    store_rows(sm.kr[0], opsA.kraw);
+    store_rows(sm.wt, opsA.wraw);
+  }
+  publish_state();
+  __syncthreads();
+
+  // One chunk; `cur` holds its operands, `nxt` receives the next chunk's
+  // (the last chunk loads itself again, so every load is unconditional).
+  auto step = [&](const FwdH8Ops& cur, FwdH8Ops& nxt, int64_t ci) {
+    const int64_t s = bos + ci * kC;
+    const int L = static_cast<int>(min<int64_t>(kC, eos - s));
+    const int64_t cidx = c0 + ci;
+    load_ops(nxt, min(ci + 1, nch - 1));
+    // Snapshot of the state entering this chunk (its bf16 hi part): lane
+    // (lg, l15) stores key 32 wr + 16 t + l15, columns cb + 8 lg .. + 7.
+    bf16* hdst = reinterpret_cast<bf16*>(p.h) + (cidx * p.H + h) * static_cast<int64_t>(K) * V + v0 + cb + 8 * lg;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int kc = wr * 32 + 16 * t;
+      const bf8_t x = cat_bf8(sb8_col4(sm.sb[0], kc, cb + 8 * lg), sb8_col4(sm.sb[0], kc, cb + 8 * lg + 4));
+      *reinterpret_cast<bf8_t*>(hdst + static_cast<int64_t>(kc + l15) * V) = x;
+    }
+    // (w S)^T: C tile hb holds columns cb + 8 lg + 4 hb + i of token 16 wr + l15.
+    f4_t ws[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const bf8_t wb = kr_a(sm.wt, wr, kk);
+#pragma unroll
+      for (int hb = 0; hb < 2; ++hb) {
+        const int vr = cb + 8 * (l15 >> 2) + 4 * hb + (l15 & 3);
+        const bf8_t sh = *reinterpret_cast<const bf8_t*>(&sm.sb[0][sb8_off(vr, kk * 32 + 8 * lg)]);
+        const bf8_t sl = *reinterpret_cast<const bf8_t*>(&sm.sb[1][sb8_off(vr, kk * 32 + 8 * lg)]);
+        ws[hb] = mfma16(sh, wb, ws[hb]);
+        ws[hb] = mfma16(sl, wb, ws[hb]);
+      }
+    }
+    const int tok = wr * 16 + l15;
+    const float dec = tok < L ? (p.gcum ? safe_exp(cur.gl - cur.gct) : 1.f) : 0.f;
+    alignas(16) float d[8];
+    bf8_t vb;
+#pragma unroll
+    for (int hb = 0; hb < 2; ++hb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float vn = static_cast<float>(cur.ut[4 * hb + i]) - ws[hb][i];
+        vb[4 * hb + i] = static_cast<__bf16>(vn);
+        d[4 * hb + i] = vn * dec;
+      }
+    if (p.vnew && tok < L)
+      *reinterpret_cast<bf8_t*>(reinterpret_cast<bf16*>(p.vnew) + (s + tok) * vrow + vcol) = vb;
+    bf8_t dh, dl;
+    split8(d, dh, dl);
+    *reinterpret_cast<bf8_t*>(&sm.dt[0][t8_off(tok, cb + 8 * lg)]) = dh;
+    *reinterpret_cast<bf8_t*>(&sm.dt[1][t8_off(tok, cb + 8 * lg)]) = dl;
+    const float egl = p.gcum ? __expf(cur.gl) : 1.f;
+    __syncthreads();  // (1) D complete; state copy and w rows read
+
+    // S <- exp(gl) S + K^T D for key rows 32 wr .., columns cb ...
+    const __bf16* kr = sm.kr[ci & 1];
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2) {
+      const int mi = wr * M2 + m2;
+      bf8_t ka[2];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) ka[kk] = kr_at(kr, mi, kk);
+#pragma unroll
+      for (int nj = 0; nj < NJ; ++nj) {
+        f4_t acc = sreg[m2][nj];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= egl;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int r0 = kk * 32 + 8 * lg;
+          const bf8_t xh = cat_bf8(t8_col4(sm.dt[0], cb + nj * 16, r0), t8_col4(sm.dt[0], cb + nj * 16, r0 + 4));
+          const bf8_t xl = cat_bf8(t8_col4(sm.dt[1], cb + nj * 16, r0), t8_col4(sm.dt[1], cb + nj * 16, r0 + 4));
+          acc = mfma16(ka[kk], xh, acc);
+          acc = mfma16(ka[kk], xl, acc);
+        }
+        sreg[m2][nj] = acc;
+      }
+    }
+    publish_state();
+    store_rows(sm.kr[(ci + 1) & 1], nxt.kraw);
+    store_rows(sm.wt, nxt.wraw);
+    __syncthreads();  // (2) state copy, next rows written; key rows and D read
+  };
+  // Unrolled by two so the operand buffers swap roles without copies.
+  for (int64_t ci = 0; ci < nch; ci += 2) {
+    step(opsA, opsB, ci);
+    if (ci + 1 < nch) step(opsB, opsA, ci + 1);
+  }
+  if (p.ht) {
+#pragma unroll
+    for (int m2 = 0; m2 < M2; ++m2)
+#pragma unroll
+      for (int nj = 0; nj < NJ; ++nj)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kr = wr * (K / 4) + m2 * 16 + 4 * lg + i;
+          p.ht[((n * p.H + h) * K + kr) * V + v0 + cb + nj * 16 + l15] = sreg[m2][nj][i];
+        }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Output: o = scale (exp(gc) (q h_c) + tril(q k^T exp(gc_i - gc_j)) v_new).
 // One block per (chunk, head): h_c and v_new staged transposed in LDS, wave
 // w owns rows [16w, 16w+16) and all V columns.
@@ -761,8 +974,9 @@ chunk_fwd_o_kernel(FwdOParams p) {
   constexpr int KK = K / 32, NJ = V / 16;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
   const int l15 = lane & 15, lg = lane >> 4;
-  const int h = blockIdx.y;
-  const int64_t c = blockIdx.x;
+  // Heads of one chunk before the next chunk (whole token rows in flight).
+  const int h = static_cast<int>(blockIdx.x % p.H);
+  const int64_t c = blockIdx.x / p.H;
   int64_t n, s;
   int L;
   if (!locate_chunk(p, c, n, s, L) || c >= p.hcap) return;  // block-uniform
@@ -980,7 +1194,9 @@ extern "C" int xk_chunk_scaled_dot_kkt(const void* k, xk_dtype dtype, const void
   p.Hg = static_cast<int>(Hg);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if ((st = launch_offsets(p, s))) return st;
-  const dim3 grid(p.NTmax, (H + 3) / 4);
+  const int64_t blocks = p.NTmax * ((H + 3) / 4);
+  if (blocks > INT32_MAX) return XK_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<uint32_t>(blocks));
   if (beta_dtype == XK_BF16)
     hipLaunchKernelGGL((chunk_kkt_kernel<128, bf16>), grid, dim3(kTh), 0, s, p);
   else
@@ -1003,7 +1219,9 @@ extern "C" int xk_solve_tril(const float* A, void* Ai, xk_dtype ai_dtype, int64_
   p.H = static_cast<int>(H);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if ((st = launch_offsets(p, s))) return st;
-  const dim3 grid(p.NTmax, (H + 3) / 4);
+  const int64_t blocks = p.NTmax * ((H + 3) / 4);
+  if (blocks > INT32_MAX) return XK_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<uint32_t>(blocks));
   switch (ai_dtype) {
     case XK_F32: hipLaunchKernelGGL(solve_tril_kernel<float>, grid, dim3(kTh), 0, s, p); break;
     case XK_BF16: hipLaunchKernelGGL(solve_tril_kernel<bf16>, grid, dim3(kTh), 0, s, p); break;
@@ -1027,8 +1245,8 @@ extern "C" int xk_recompute_w_u(const void* k, const void* v, xk_dtype dtype, co
   if (ai_dtype != XK_BF16 && ai_dtype != XK_F32) return XK_ERR_UNSUPPORTED;
   if (N == 0 || total_tokens == 0) return XK_OK;
   if (!k || !v || !beta || !Ai || !w || !u || !cu_seqlens) return XK_ERR_INVALID;
-  if (!aligned(k, 16) || !aligned(v, 16) || !aligned(Ai, 16) || !aligned(w, 8) ||
-      !aligned(u, 8))
+  if (!aligned(k, 16) || !aligned(v, 16) || !aligned(Ai, 16) || !aligned(w, 16) ||
+      !aligned(u, 16))
     return XK_ERR_INVALID;
   p.k = k;
   p.v = v;
@@ -1041,7 +1259,8 @@ extern "C" int xk_recompute_w_u(const void* k, const void* v, xk_dtype dtype, co
   p.Hg = static_cast<int>(Hg);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if ((st = launch_offsets(p, s))) return st;
-  const dim3 grid(p.NTmax, H);
+  if (p.NTmax * H > INT32_MAX) return XK_ERR_UNSUPPORTED;
+  const dim3 grid(static_cast<uint32_t>(p.NTmax * H));
   if (beta_dtype == XK_BF16) {
     if (ai_dtype == XK_BF16) hipLaunchKernelGGL((recompute_w_u_kernel<bf16, bf16>), grid, dim3(kTh), 0, s, p);
     else hipLaunchKernelGGL((recompute_w_u_kernel<bf16, float>), grid, dim3(kTh), 0, s, p);
@@ -1077,11 +1296,18 @@ extern "C" int xk_chunk_fwd_h(const void* k, const void* w, const void* u, xk_dt
   p.ht = final_state;
   p.H = static_cast<int>(H);
   p.Hg = static_cast<int>(Hg);
-  p.nvt = static_cast<int>(V / kBV);
+  // 64-column tiles (16-byte accesses of u, v_new and h) where V and the
+  // alignment allow, else 32-column tiles.
+  const bool wide = V % 64 == 0 && aligned(u, 16) && aligned(h, 16) && aligned(v_new, 16);
+  p.nvt = static_cast<int>(V / (wide ? 64 : kBV));
   hipStream_t s = static_cast<hipStream_t>(stream);
   if ((st = launch_offsets(p, s, true))) return st;
   const int64_t blocks = cdiv(N * H, 8) * 8 * p.nvt;
-  hipLaunchKernelGGL(chunk_fwd_h_kernel<128>, dim3(blocks), dim3(kTh), 0, s, p);
+  if (blocks > INT32_MAX) return XK_ERR_UNSUPPORTED;
+  if (wide)
+    hipLaunchKernelGGL(chunk_fwd_h8_kernel<128>, dim3(static_cast<uint32_t>(blocks)), dim3(kTh8), 0, s, p);
+  else
+    hipLaunchKernelGGL(chunk_fwd_h_kernel<128>, dim3(static_cast<uint32_t>(blocks)), dim3(kTh), 0, s, p);
   return launch_status();
 }
 
@@ -1112,6 +1338,8 @@ extern "C" int xk_chunk_fwd_o(const void* q, const void* k, const void* v, const
   p.Hg = static_cast<int>(Hg);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if ((st = launch_offsets(p, s))) return st;
-  hipLaunchKernelGGL((chunk_fwd_o_kernel<128, 128>), dim3(p.NTmax, H), dim3(kTh), 0, s, p);
+  if (p.NTmax * H > INT32_MAX) return XK_ERR_UNSUPPORTED;
+  hipLaunchKernelGGL((chunk_fwd_o_kernel<128, 128>), dim3(static_cast<uint32_t>(p.NTmax * H)),
+                     dim3(kTh), 0, s, p);
   return launch_status();
 }
