@@ -728,9 +728,11 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
 //                             the two C tiles of a lane; B: w rows)
 //   h snapshot               (the state copy's hi part read transposed)
 // and D = v_new * decay goes to LDS as token rows, read transposed as the B
-// operand of S <- exp(gl) S + K^T D.  Two barriers per chunk.  Key and w
-// rows are loaded a chunk ahead into registers (whole rows, 16 lanes a
-// row) and written to LDS at the end of the chunk before.
+// operand of S <- exp(gl) S + K^T D.  Two barriers per chunk.  A chunk's
+// operands are loaded two chunks ahead into registers (key and w rows
+// whole, 16 lanes a row); its key and w rows go to LDS at the end of the
+// chunk before, so each load has a whole chunk to land before anything
+// waits for it.
 // ---------------------------------------------------------------------------
 constexpr int kTh8 = 512;
 
@@ -747,6 +749,15 @@ struct FwdH8Ops {
   bf8_t ut;                // u of token 16 wr + lane % 16, columns cb + 8 (lane / 16) .. + 7
   float gct;               // gc of that token
   float gl;                // gc of the chunk's last token
+};
+// The register operands of a chunk, computed from its FwdH8Ops at the end of
+// the chunk before (where that chunk's loads are waited for anyway), so the
+// chunk itself reads no load destination: the compiler's memory-counter
+// waits at a loop-carried load were conservative and held up the chunk.
+struct FwdH8Carry {
+  float u[8];  // ut as fp32
+  float dg;    // gl - gct
+  float egl;   // exp(gl)
 };
 
 template <int K>
@@ -770,7 +781,8 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
   const int V = p.nvt * 64, v0 = vt * 64;
   const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
   const int64_t c0 = p.chunk_off[n];
-  const int64_t nch = max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.hcap - c0));
+  // Chunk counters are 32-bit (scalar compares; a sequence has < 2^31 chunks).
+  const int nch = static_cast<int>(max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.hcap - c0)));
 
   f4_t sreg[M2][NJ];
 #pragma unroll
@@ -798,8 +810,8 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
   const uint32_t wrb = static_cast<uint32_t>(p.H) * K * 2;   // w row bytes
   const int64_t vrow = static_cast<int64_t>(p.H) * V;         // u / v_new row elements
   const int vcol = h * V + v0 + cb + 8 * lg;                   // this lane's u / v_new columns
-  auto load_ops = [&](FwdH8Ops& o, int64_t ci) {
-    const int64_t s = bos + ci * kC;
+  auto load_ops = [&](FwdH8Ops& o, int ci) {
+    const int64_t s = bos + static_cast<int64_t>(ci) * kC;
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
     const char* kb = reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.k) + (s * p.Hg + hq) * K);
     const char* wb = reinterpret_cast<const char*>(reinterpret_cast<const bf16*>(p.w) + (s * p.H + h) * K);
@@ -820,22 +832,39 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
       *reinterpret_cast<bf8_t*>(tile + kr_off(wr * 16 + cg * 8 + 4 * j + rl, ch)) = raw[j];
   };
 
-  FwdH8Ops opsA, opsB;
+  // The empty asm statements pin the values here: without them the
+  // conversions sink to their uses in the next chunk.
+  auto carry = [&](FwdH8Carry& c, const FwdH8Ops& o) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      c.u[e] = static_cast<float>(o.ut[e]);
+      asm volatile("" : "+v"(c.u[e]));
+    }
+    c.dg = o.gl - o.gct;
+    c.egl = p.gcum ? __expf(o.gl) : 1.f;
+    asm volatile("" : "+v"(c.dg), "+v"(c.egl));
+  };
+  FwdH8Ops opsA, opsB, opsC;
+  FwdH8Carry cy;
   if (nch > 0) {
     load_ops(opsA, 0);
+    load_ops(opsB, min(1, nch - 1));
     store_rows(sm.kr[0], opsA.kraw);
     store_rows(sm.wt, opsA.wraw);
+    carry(cy, opsA);
   }
   publish_state();
   __syncthreads();
 
-  // One chunk; `cur` holds its operands, `nxt` receives the next chunk's
-  // (the last chunk loads itself again, so every load is unconditional).
-  auto step = [&](const FwdH8Ops& cur, FwdH8Ops& nxt, int64_t ci) {
-    const int64_t s = bos + ci * kC;
+  // One chunk; `cy` holds its register operands, `mid` the next chunk's
+  // operands (its rows go to LDS and its carry to `cy` at the end), `far`
+  // receives the chunk after that (past the last chunk the last one loads
+  // again, so every load is unconditional).
+  auto step = [&](const FwdH8Ops& mid, FwdH8Ops& far, int ci) {
+    const int64_t s = bos + static_cast<int64_t>(ci) * kC;
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
     const int64_t cidx = c0 + ci;
-    load_ops(nxt, min(ci + 1, nch - 1));
+    load_ops(far, min(ci + 2, nch - 1));
     // Snapshot of the state entering this chunk (its bf16 hi part): lane
     // (lg, l15) stores key 32 wr + 16 t + l15, columns cb + 8 lg .. + 7.
     bf16* hdst = reinterpret_cast<bf16*>(p.h) + (cidx * p.H + h) * static_cast<int64_t>(K) * V + v0 + cb + 8 * lg;
@@ -860,14 +889,14 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
       }
     }
     const int tok = wr * 16 + l15;
-    const float dec = tok < L ? (p.gcum ? safe_exp(cur.gl - cur.gct) : 1.f) : 0.f;
+    const float dec = tok < L ? (p.gcum ? safe_exp(cy.dg) : 1.f) : 0.f;
     alignas(16) float d[8];
     bf8_t vb;
 #pragma unroll
     for (int hb = 0; hb < 2; ++hb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float vn = static_cast<float>(cur.ut[4 * hb + i]) - ws[hb][i];
+        const float vn = cy.u[4 * hb + i] - ws[hb][i];
         vb[4 * hb + i] = static_cast<__bf16>(vn);
         d[4 * hb + i] = vn * dec;
       }
@@ -877,7 +906,7 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
     split8(d, dh, dl);
     *reinterpret_cast<bf8_t*>(&sm.dt[0][t8_off(tok, cb + 8 * lg)]) = dh;
     *reinterpret_cast<bf8_t*>(&sm.dt[1][t8_off(tok, cb + 8 * lg)]) = dl;
-    const float egl = p.gcum ? __expf(cur.gl) : 1.f;
+    const float egl = cy.egl;
     __syncthreads();  // (1) D complete; state copy and w rows read
 
     // S <- exp(gl) S + K^T D for key rows 32 wr .., columns cb ...
@@ -905,15 +934,22 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
       }
     }
     publish_state();
-    store_rows(sm.kr[(ci + 1) & 1], nxt.kraw);
-    store_rows(sm.wt, nxt.wraw);
+    store_rows(sm.kr[(ci + 1) & 1], mid.kraw);
+    store_rows(sm.wt, mid.wraw);
+    carry(cy, mid);
     __syncthreads();  // (2) state copy, next rows written; key rows and D read
   };
-  // Unrolled by two so the operand buffers swap roles without copies.
-  for (int64_t ci = 0; ci < nch; ci += 2) {
-    step(opsA, opsB, ci);
-    if (ci + 1 < nch) step(opsB, opsA, ci + 1);
+  // Unrolled by three so the operand buffers rotate without copies; the
+  // loop body has no branches around steps (the compiler's memory-counter
+  // waits then follow the rotation), the last one or two chunks follow it.
+  int ci = 0;
+  for (; ci + 2 < nch; ci += 3) {
+    step(opsB, opsC, ci);
+    step(opsC, opsA, ci + 1);
+    step(opsA, opsB, ci + 2);
   }
+  if (ci < nch) step(opsB, opsC, ci);
+  if (ci + 1 < nch) step(opsC, opsA, ci + 1);
   if (p.ht) {
 #pragma unroll
     for (int m2 = 0; m2 < M2; ++m2)
