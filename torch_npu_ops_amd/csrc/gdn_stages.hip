@@ -374,21 +374,27 @@ constexpr int kLt = kC + 8;  // bf16 LDS row stride (144 B: 16-byte aligned)
 // products.  The per-token factors are folded into Ai's columns,
 // u = (Ai diag(b)) v and w = (Ai diag(b exp(gc))) k, so the right-hand
 // sides are the raw bf16 rows: they go from HBM straight into LDS tiles by
-// direct loads (no registers, no conversion), while each lane loads its
-// Ai row, and the block waits once for all of it.  The scaled Ai rows are
-// split hi / lo in registers (fp32 to ~2^-16) and are the B operands of both
-// products, formed transposed, out^T = rhs^T Ai'^T, so that a lane owns one
-// token and (through kr_at_pair's column order) 8 consecutive columns of it:
-// 16-byte stores.  Factors of key tokens >= L are 0, so those rows of the
-// tiles (copies of row L - 1) add nothing.  Ai is lower triangular, so
-// waves 0 and 1 skip the key tokens 32 .. 63.
+// direct loads (no registers, no conversion), whole rows at a time like the
+// chunk's Ai rows, and the block waits once for all of it (Ai through
+// registers, a quad reading four rows: 129.0 -> 124.5 us at config 4 on
+// MI355X).  The scaled Ai rows are split hi / lo in registers (fp32 to
+// ~2^-16) and are the B operands of both products, formed transposed,
+// out^T = rhs^T Ai'^T, so that a lane owns one token and (through
+// kr_at_pair's column order) 8 consecutive columns of it: 16-byte stores.
+// Factors of key tokens >= L are 0, so those rows of the tiles (copies of
+// row L - 1) add nothing.  Ai is lower triangular, so waves 0 and 1 skip
+// the key tokens 32 .. 63.
 template <typename BT, typename AT>
 __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
   constexpr int D = 128;  // K = V = 128
   static_assert(D == kKrRow, "row tiles of 128 bf16");
   __shared__ __align__(16) __bf16 vt[kC * D];  // v rows (kr_off layout)
   __shared__ __align__(16) __bf16 kt[kC * D];  // k rows (kr_off layout)
+  __shared__ __align__(16) AT at[kC * kC];     // Ai rows, 16-byte chunk c of row r at c ^ (r % CPR)
   __shared__ __align__(16) float fb[kC], fk[kC];
+  constexpr int CE = 16 / static_cast<int>(sizeof(AT));  // Ai elements per 16-byte chunk
+  constexpr int CPR = kC / CE;                           // chunks per Ai row
+  constexpr int RPI = 64 / CPR;                          // Ai rows per 1 KB load
   // Blocks take the heads of one chunk before the next chunk, so that the
   // blocks in flight read whole token rows.
   const int h = static_cast<int>(blockIdx.x % p.H);
@@ -408,14 +414,19 @@ __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
     dma16(reinterpret_cast<const bf16*>(p.v) + (t * p.H + h) * D + 8 * c, vt + (wid * 16 + 4 * j) * D);
     dma16(reinterpret_cast<const bf16*>(p.k) + (t * p.Hg + hq) * D + 8 * c, kt + (wid * 16 + 4 * j) * D);
   }
-  // Ai row tq, keys 32 kk + 8 lg .. + 7 (B operand layout).
-  const int tq = wid * 16 + l15;
-  const AT* arow = reinterpret_cast<const AT*>(p.Ai) + ((s + min(tq, L - 1)) * p.H + h) * kC + 8 * lg;
-  float ai[2][8];
+  // Ai rows 16w .. 16w + 15 whole (CPR lanes a row), likewise.
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) load_vec_f32<AT, 8>(arow + 32 * kk, ai[kk]);
+  for (int j = 0; j < 16 / RPI; ++j) {
+    const int r = wid * 16 + RPI * j + lane / CPR;
+    const int c = (lane % CPR) ^ (r % CPR);
+    dma16(reinterpret_cast<const AT*>(p.Ai) + ((s + min(r, L - 1)) * p.H + h) * kC + CE * c,
+          at + (wid * 16 + RPI * j) * kC);
+  }
+  const int tq = wid * 16 + l15;
   // The 64 token factors (lane = token), loaded last so that their wait
-  // overlaps the loads above.
+  // overlaps the loads above.  (Fetching them by shuffles instead, which
+  // brings the LDS to 40 KB and four blocks per CU with bf16 Ai, measured
+  // 128.1 against 124.5 us at config 4 on MI355X.)
   const int64_t ft = (s + min(lane, L - 1)) * p.H + h;
   const float bval = ldf<BT>(p.beta, ft);
   const float gval = p.gcum ? p.gcum[ft] : 0.f;
@@ -424,6 +435,24 @@ __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
     fk[lane] = lane < L ? bval * __expf(gval) : 0.f;
   }
   dma_sync();  // tiles, Ai rows and factors
+
+  // Ai row tq, keys 32 kk + 8 lg .. + 7 (B operand layout).
+  float ai[2][8];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int h8 = 0; h8 < 8 / CE; ++h8) {
+      const int c = (32 * kk + 8 * lg) / CE + h8;
+      const AT* src = at + tq * kC + CE * (c ^ (tq % CPR));
+      if constexpr (CE == 8) {
+        load_vec_f32<AT, 8>(src, ai[kk]);
+      } else {
+        float t4[4];
+        load_vec_f32<AT, 4>(src, t4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ai[kk][4 * h8 + e] = t4[e];
+      }
+    }
 
   bf8_t uh[2], ul[2], wh[2], wl[2];
 #pragma unroll
@@ -983,7 +1012,7 @@ struct FwdOParams : Seq {
 template <int K, int V>
 struct __align__(16) FwdOSmem {
   __bf16 hr[K * V];   // h_c rows hr[k][v] (kr_off layout)
-  __bf16 vr[kC * V];  // v_new rows vr[token][v] (kr_off layout); rows >= L zero
+  __bf16 vr[kC * V];  // v_new rows vr[token][v] (kr_off layout); rows >= L repeat row L - 1
   float gc[kC];
 };
 
@@ -1008,7 +1037,7 @@ chunk_fwd_o_kernel(FwdOParams p) {
   static_assert(K == 128 && V == 128, "head dims of 128");
   __shared__ FwdOSmem<K, V> sm;
   constexpr int KK = K / 32, NJ = V / 16;
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, wid = wave_index(), lane = tid & 63;
   const int l15 = lane & 15, lg = lane >> 4;
   // Heads of one chunk before the next chunk (whole token rows in flight).
   const int h = static_cast<int>(blockIdx.x % p.H);
@@ -1019,33 +1048,28 @@ chunk_fwd_o_kernel(FwdOParams p) {
   const int hq = h / (p.H / p.Hg);
   const f4_t zero = {0.f, 0.f, 0.f, 0.f};
 
-  // Every global operand is loaded before its first use: h and v_new rows,
-  // then q and the key tiles of Aq, which stay in flight across the
-  // barrier.  Each 16 lanes load one whole 256-byte row.
+  // Every global operand is loaded before its first use.  h and v_new rows
+  // go straight into their LDS tiles by direct loads (1 KB = 4 whole rows a
+  // load; LDS chunk lane % 16 of row r holds the row's chunk
+  // (lane % 16) ^ (r % 16)); v_new rows >= L repeat row L - 1, which the
+  // masked Aq multiplies by 0.  q and the key tiles of Aq follow in
+  // registers.
   static_assert(V == kKrRow, "row tiles of 128 bf16");
   const int rl = lane >> 4, ch = lane & 15;  // row within a load, 16-byte chunk
   const bf16* hsrc = reinterpret_cast<const bf16*>(p.h) + (c * p.H + h) * static_cast<int64_t>(K) * V;
-  bf8_t hv[8];  // h_c rows 32w + 4j + rl
 #pragma unroll
-  for (int j = 0; j < 8; ++j)
-    hv[j] = *reinterpret_cast<const bf8_t*>(hsrc + (wid * 32 + 4 * j + rl) * V + 8 * ch);
-  bf8_t vv[4];  // v_new rows (tokens) 16w + 4j + rl
+  for (int j = 0; j < 8; ++j) {
+    const int r = wid * 32 + 4 * j + rl;
+    dma16(hsrc + r * V + 8 * (ch ^ (r & 15)), sm.hr + (wid * 32 + 4 * j) * V);
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int t = wid * 16 + 4 * j + rl;
-    vv[j] = *reinterpret_cast<const bf8_t*>(reinterpret_cast<const bf16*>(p.v) +
-                                            ((s + min(t, L - 1)) * p.H + h) * static_cast<int64_t>(V) +
-                                            8 * ch);
+    dma16(reinterpret_cast<const bf16*>(p.v) + ((s + min(t, L - 1)) * p.H + h) * static_cast<int64_t>(V) +
+              8 * (ch ^ (t & 15)),
+          sm.vr + (wid * 16 + 4 * j) * V);
   }
-#pragma unroll
-  for (int j = 0; j < 8; ++j)
-    *reinterpret_cast<bf8_t*>(sm.hr + kr_off(wid * 32 + 4 * j + rl, ch)) = hv[j];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int t = wid * 16 + 4 * j + rl;
-    *reinterpret_cast<bf8_t*>(sm.vr + kr_off(t, ch)) = t < L ? vv[j] : bf8_t{};
-  }
-  if (tid < kC) sm.gc[tid] = p.gcum ? p.gcum[(s + min(tid, L - 1)) * p.H + h] : 0.f;
+  const float gct = p.gcum ? p.gcum[(s + min(lane, L - 1)) * p.H + h] : 0.f;
   const int64_t qrow = static_cast<int64_t>(p.Hg) * K;
   const int tq = wid * 16 + l15;  // this lane's output token
   // q rows and the key rows of Aq, loaded quad-contiguously (q4_load; rows
@@ -1056,13 +1080,16 @@ chunk_fwd_o_kernel(FwdOParams p) {
   const bf16* kbase = reinterpret_cast<const bf16*>(p.k) + static_cast<int64_t>(hq) * K;
   bf8_t qa[KK], ka[4][KK];
   q4_load([&](int r) { return qbase + (s + min(wid * 16 + r, L - 1)) * qrow; }, qa);
+  // Key tiles j <= w only (Aq is lower triangular).
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    q4_load([&](int r) { return kbase + (s + min(j * 16 + r, L - 1)) * qrow; }, ka[j]);
-  __syncthreads();
+    if (j <= wid) q4_load([&](int r) { return kbase + (s + min(j * 16 + r, L - 1)) * qrow; }, ka[j]);
+  if (wid == 0) sm.gc[lane] = gct;
+  dma_sync();
   q4_to_a(qa);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) q4_to_a(ka[j]);
+  for (int j = 0; j < 4; ++j)
+    if (j <= wid) q4_to_a(ka[j]);
 
   const float gq = sm.gc[tq];
 
