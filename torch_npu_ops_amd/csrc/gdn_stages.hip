@@ -894,15 +894,6 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
     const int L = static_cast<int>(min<int64_t>(kC, eos - s));
     const int64_t cidx = c0 + ci;
     load_ops(far, min(ci + 2, nch - 1));
-    // Snapshot of the state entering this chunk (its bf16 hi part): lane
-    // (lg, l15) stores key 32 wr + 16 t + l15, columns cb + 8 lg .. + 7.
-    bf16* hdst = reinterpret_cast<bf16*>(p.h) + (cidx * p.H + h) * static_cast<int64_t>(K) * V + v0 + cb + 8 * lg;
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int kc = wr * 32 + 16 * t;
-      const bf8_t x = cat_bf8(sb8_col4(sm.sb[0], kc, cb + 8 * lg), sb8_col4(sm.sb[0], kc, cb + 8 * lg + 4));
-      *reinterpret_cast<bf8_t*>(hdst + static_cast<int64_t>(kc + l15) * V) = x;
-    }
     // (w S)^T: C tile hb holds columns cb + 8 lg + 4 hb + i of token 16 wr + l15.
     f4_t ws[2] = {f4_t{0.f, 0.f, 0.f, 0.f}, f4_t{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -929,8 +920,6 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
         vb[4 * hb + i] = static_cast<__bf16>(vn);
         d[4 * hb + i] = vn * dec;
       }
-    if (p.vnew && tok < L)
-      *reinterpret_cast<bf8_t*>(reinterpret_cast<bf16*>(p.vnew) + (s + tok) * vrow + vcol) = vb;
     bf8_t dh, dl;
     split8(d, dh, dl);
     *reinterpret_cast<bf8_t*>(&sm.dt[0][t8_off(tok, cb + 8 * lg)]) = dh;
@@ -938,6 +927,21 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
     const float egl = cy.egl;
     __syncthreads();  // (1) D complete; state copy and w rows read
 
+    // The chunk's global stores are issued here, beside the state update,
+    // rather than in the chain before barrier (1): 240 -> 199 us at config 4
+    // on MI355X.
+    if (p.vnew && tok < L)
+      *reinterpret_cast<bf8_t*>(reinterpret_cast<bf16*>(p.vnew) + (s + tok) * vrow + vcol) = vb;
+    // Snapshot of the state entering this chunk (its bf16 hi part, still in
+    // the state copy until publish_state below): lane (lg, l15) stores key
+    // 32 wr + 16 t + l15, columns cb + 8 lg .. + 7.
+    bf16* hdst = reinterpret_cast<bf16*>(p.h) + (cidx * p.H + h) * static_cast<int64_t>(K) * V + v0 + cb + 8 * lg;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int kc = wr * 32 + 16 * t;
+      const bf8_t x = cat_bf8(sb8_col4(sm.sb[0], kc, cb + 8 * lg), sb8_col4(sm.sb[0], kc, cb + 8 * lg + 4));
+      *reinterpret_cast<bf8_t*>(hdst + static_cast<int64_t>(kc + l15) * V) = x;
+    }
     // S <- exp(gl) S + K^T D for key rows 32 wr .., columns cb ...
     const __bf16* kr = sm.kr[ci & 1];
 #pragma unroll
