@@ -134,11 +134,19 @@ def test_prefill_workload_l2norm_in_op(dev):
     _check(dev, q, k, v, g, beta, h0, cu, True, heads=[0, 1, 17, 31])
 
 
+def _many(n, seed):
+    """cu_seqlens of n sequences of 0..70 tokens."""
+    lens = torch.randint(0, 71, (n,), generator=torch.Generator().manual_seed(seed))
+    return [0] + torch.cumsum(lens, 0).tolist()
+
+
 @pytest.mark.parametrize("cu_list", [
     [0, 0, 70, 71, 150],          # empty and one-token sequences
     [0, 64, 128, 193, 193, 257],  # chunk-boundary lengths, empty in the middle
     [0, 1],
     [0, 63, 127, 300],
+    _many(64, 7),                 # chunks found within a wave (up to 64 sequences)
+    _many(80, 8),                 # chunks from the offsets kernel's table
 ])
 def test_varlen_edges(dev, cu_list):
     cu = torch.tensor(cu_list, dtype=torch.int32)

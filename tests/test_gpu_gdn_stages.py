@@ -22,10 +22,23 @@ pytestmark = pytest.mark.gpu
 F32_TOL = dict(rtol=1e-3, atol=1e-3)
 O_TOL = dict(rtol=1.6e-2, atol=1e-2)
 
+
+
+def _many(n, seed):
+    """cu_seqlens of n sequences of 0..70 tokens (empty, one-token and
+    two-chunk ones among them)."""
+    lens = torch.randint(0, 71, (n,), generator=torch.Generator().manual_seed(seed))
+    return [0] + torch.cumsum(lens, 0).tolist()
+
+
+# Up to 64 sequences the kernels find their chunks within a wave; past that
+# they read the offsets kernel's table (both sides of the switch are here).
 CU_CASES = [
     [0, 1, 65, 130, 300],
     [0, 0, 64, 64, 200],
     [0, 4096],
+    _many(64, 5),
+    _many(80, 6),
 ]
 
 

@@ -153,9 +153,16 @@ __global__ void __launch_bounds__(kTh) gdn_chunk_prep_kernel(ChunkParams p) {
   const int hg4 = (p.HV + 3) >> 2;
   const int64_t c = blockIdx.x / hg4;
   const int hv = static_cast<int>(blockIdx.x % hg4) * 4 + wid;
-  const int2 ce = p.ctab[c];  // (first token, length); length 0 past the last chunk
-  const int64_t s = ce.x;
-  const int L = ce.y;
+  int64_t s;
+  int L;
+  if (p.N <= kWaveSeqs) {
+    int64_t n;
+    if (!wave_locate_chunk(p, c, n, s, L)) L = 0;
+  } else {
+    const int2 ce = p.ctab[c];  // (first token, length); length 0 past the last chunk
+    s = ce.x;
+    L = ce.y;
+  }
   // Wave-uniform exit; the kernel has no block-level barriers.
   if (!(hv < p.HV && L > 0)) return;
   float (*X)[kLd] = lds[wid];
@@ -429,13 +436,13 @@ gdn_chunk_state_kernel(ChunkParams p, int nvt) {
   const int vt = static_cast<int>(r % nvt);
   const int64_t item = (r / nvt) * 8 + xcd;  // (sequence rank, head) index
   if (item >= p.N * p.HV) return;            // whole block
-  const int64_t n = p.seq_order[item / p.HV];
+  int64_t n, cidx0;
+  find_ranked_seq(p, item / p.HV, n, cidx0);
   const int hv = state_head(static_cast<int>(item % p.HV), p.HV, p.H);
   const int hq = hv / (p.HV / p.H);
   const int V = nvt * BV;
   const int v0 = vt * BV;
   const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
-  const int64_t cidx0 = p.chunk_off[n];
   // Chunks of this sequence; the NTmax bound keeps a malformed cu_seqlens
   // (never a well-formed one) from reading past the workspace.
   const int64_t nch = max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.NTmax - cidx0));
@@ -727,13 +734,13 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
   const int vt = static_cast<int>(r % nvt);
   const int64_t item = (r / nvt) * 8 + xcd;
   if (item >= p.N * p.HV) return;
-  const int64_t n = p.seq_order[item / p.HV];
+  int64_t n, cidx0;
+  find_ranked_seq(p, item / p.HV, n, cidx0);
   const int hv = state_head(static_cast<int>(item % p.HV), p.HV, p.H);
   const int hq = hv / (p.HV / p.H);
   const int V = nvt * BV;
   const int v0 = vt * BV;
   const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
-  const int64_t cidx0 = p.chunk_off[n];
   const int64_t nch = max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.NTmax - cidx0));
 
   constexpr int M2 = K / 64;
@@ -981,10 +988,12 @@ gdn_chunk_state8_kernel(ChunkParams p, int nvt) {
 
 template <int K, typename GT, typename BT>
 int launch_chunk(const ChunkParams& p, int64_t V, hipStream_t s) {
-  hipLaunchKernelGGL(chunk_offsets_kernel<ChunkParams>, dim3(1), dim3(256), 0, s, p,
-                     p.seq_order, p.ctab, p.NTmax);
-  int st = launch_status();
-  if (st) return st;
+  int st;
+  if (p.N > kWaveSeqs) {  // else the kernels look chunks up themselves
+    hipLaunchKernelGGL(chunk_offsets_kernel<ChunkParams>, dim3(1), dim3(256), 0, s, p,
+                       p.seq_order, p.ctab, p.NTmax);
+    if ((st = launch_status())) return st;
+  }
   const int64_t prep_blocks = p.NTmax * ((p.HV + 3) / 4);
   if (prep_blocks > INT32_MAX) return XK_ERR_UNSUPPORTED;
   hipLaunchKernelGGL((gdn_chunk_prep_kernel<K, GT, BT>), dim3(static_cast<uint32_t>(prep_blocks)),

@@ -494,6 +494,104 @@ __device__ __forceinline__ bool locate_chunk(const P& p, int64_t c, int64_t& n, 
   return true;
 }
 
+// Up to kWaveSeqs sequences, a kernel finds its chunk or its sequence from
+// cu_seqlens within each wave (lane m reads sequence m), and no offsets
+// kernel runs before it: one round of loads at the start of every block
+// instead of the dependent loads of a binary search over chunk_off, and one
+// launch less per call.  Every lane of the wave must be active.
+constexpr int64_t kWaveSeqs = 64;
+
+// Inclusive wave64 prefix sum on DPP moves (no LDS round trips): shifts by
+// 1, 2, 4, 8 within each 16-lane row (lanes shifted in from outside the row
+// read 0), then row 0's total into row 1 and row 2's into row 3
+// (row_bcast:15), then lane 31's running total into rows 2 and 3
+// (row_bcast:31).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int32_t dpp_i32(int32_t v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xF, true);
+}
+__device__ __forceinline__ int32_t wave_incl_scan(int32_t x) {
+  x += dpp_i32<0x111>(x);       // row_shr:1
+  x += dpp_i32<0x112>(x);       // row_shr:2
+  x += dpp_i32<0x114>(x);       // row_shr:4
+  x += dpp_i32<0x118>(x);       // row_shr:8
+  x += dpp_i32<0x142, 0xA>(x);  // row_bcast:15 into rows 1, 3
+  x += dpp_i32<0x143, 0xC>(x);  // row_bcast:31 into rows 2, 3
+  return x;
+}
+
+struct WaveSeqs {
+  int64_t a, b;  // sequence lane's first and end token (0, 0 past N)
+  int32_t cnt;   // its chunks
+  int32_t incl;  // chunks of sequences 0 .. lane (inclusive scan)
+};
+template <class P>
+__device__ __forceinline__ WaveSeqs wave_seqs(const P& p) {
+  const int lane = threadIdx.x & (kWave - 1);
+  WaveSeqs w;
+  const bool in = lane < p.N;
+  w.a = in ? cu_at(p, lane) : 0;
+  w.b = in ? cu_at(p, lane + 1) : 0;
+  const int64_t len = w.b - w.a;
+  w.cnt = static_cast<int32_t>(len > 0 ? (len + kC - 1) / kC : 0);
+  w.incl = wave_incl_scan(w.cnt);
+  return w;
+}
+__device__ __forceinline__ int64_t readlane64(int64_t v, int l) {
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<uint32_t>(v), l);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<uint32_t>(static_cast<uint64_t>(v) >> 32), l);
+  return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// locate_chunk for N <= kWaveSeqs (wave-uniform results).
+template <class P>
+__device__ __forceinline__ bool wave_locate_chunk(const P& p, int64_t c, int64_t& n, int64_t& s,
+                                                  int& L) {
+  const WaveSeqs w = wave_seqs(p);
+  const int32_t total = __builtin_amdgcn_readlane(w.incl, kWave - 1);
+  if (c >= total) return false;
+  // Sequences that end at or before chunk c form a prefix of the lanes.
+  const int nn = __popcll(__ballot(w.incl <= c));
+  n = nn;
+  const int32_t off = __builtin_amdgcn_readlane(w.incl - w.cnt, nn);
+  s = readlane64(w.a, nn) + (c - off) * kC;
+  L = static_cast<int>(min<int64_t>(kC, readlane64(w.b, nn) - s));
+  return true;
+}
+
+// The sequence of rank r, longest first with ties by index (the order of
+// chunk_offsets_kernel), and its first global chunk, for N <= kWaveSeqs.
+template <class P>
+__device__ __forceinline__ void wave_rank_seq(const P& p, int64_t r, int64_t& n, int64_t& c0) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const WaveSeqs w = wave_seqs(p);
+  int32_t rank = 0;
+  for (int m = 0; m < static_cast<int>(p.N); ++m) {
+    const int32_t cm = __builtin_amdgcn_readlane(w.cnt, m);
+    rank += (cm > w.cnt) || (cm == w.cnt && m < lane);
+  }
+  const uint64_t hit = __ballot(lane < p.N && rank == r);
+  const int nn = hit ? static_cast<int>(__builtin_ctzll(hit)) : 0;
+  n = nn;
+  c0 = __builtin_amdgcn_readlane(w.incl - w.cnt, nn);
+}
+
+// Chunk and sequence lookups that take the wave path when N allows and
+// else read what chunk_offsets_kernel wrote.
+template <class P>
+__device__ __forceinline__ bool find_chunk(const P& p, int64_t c, int64_t& n, int64_t& s, int& L) {
+  return p.N <= kWaveSeqs ? wave_locate_chunk(p, c, n, s, L) : locate_chunk(p, c, n, s, L);
+}
+template <class P>
+__device__ __forceinline__ void find_ranked_seq(const P& p, int64_t r, int64_t& n, int64_t& c0) {
+  if (p.N <= kWaveSeqs) {
+    wave_rank_seq(p, r, n, c0);
+  } else {
+    n = p.seq_order[r];
+    c0 = p.chunk_off[n];
+  }
+}
+
 // 16x16x16 bf16 MFMA: lane l holds A[l%16][4(l/16)+e], B[4(l/16)+e][l%16]
 // and C[4(l/16)+i][l%16], so a C fragment is already a B operand.
 __device__ __forceinline__ f4_t mfma16k16(s4_t a, s4_t b, f4_t c) {

@@ -250,7 +250,8 @@ __global__ void __launch_bounds__(kTh) chunk_kkt_kernel(KktParams p) {
   const int h = static_cast<int>(blockIdx.x % hg4) * 4 + wid;
   int64_t n, s;
   int L;
-  if (!(h < p.H && locate_chunk(p, blockIdx.x / hg4, n, s, L))) return;  // wave-uniform
+  const bool found = find_chunk(p, blockIdx.x / hg4, n, s, L);
+  if (!(h < p.H && found)) return;  // wave-uniform
   const int hq = h / (p.H / p.Hg);
   constexpr int KK = K / 32;
   // Key rows loaded quad-contiguously (q4_load; rows >= L repeat row L-1)
@@ -319,7 +320,8 @@ __global__ void __launch_bounds__(kTh) solve_tril_kernel(TrilParams p) {
   const int h = static_cast<int>(blockIdx.x % hg4) * 4 + wid;
   int64_t n, s;
   int L;
-  if (!(h < p.H && locate_chunk(p, blockIdx.x / hg4, n, s, L))) return;  // wave-uniform
+  const bool found = find_chunk(p, blockIdx.x / hg4, n, s, L);
+  if (!(h < p.H && found)) return;  // wave-uniform
   float (*X)[kLd] = lds[wid];
   // Access j covers rows 8j .. 8j + 7 (lane: row 8j + lane / 8, columns
   // 8 (lane % 8) .. + 7), so every instruction moves whole rows.  Strictly
@@ -400,7 +402,7 @@ __global__ void __launch_bounds__(kTh) recompute_w_u_kernel(WuParams p) {
   const int h = static_cast<int>(blockIdx.x % p.H);
   int64_t n, s;
   int L;
-  if (!locate_chunk(p, blockIdx.x / p.H, n, s, L)) return;  // block-uniform
+  if (!find_chunk(p, blockIdx.x / p.H, n, s, L)) return;  // block-uniform
   const int hq = h / (p.H / p.Hg);
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int l15 = lane & 15, lg = lane >> 4;
@@ -558,12 +560,12 @@ __global__ void __launch_bounds__(kTh) chunk_fwd_h_kernel(FwdHParams p) {
   if (item >= p.N * p.H) return;
   // Items are dispatched longest sequence first: the longest chains start in
   // the first wave of resident blocks and shorter ones fill in behind them.
-  const int64_t n = p.seq_order[item / p.H];
+  int64_t n, c0;
+  find_ranked_seq(p, item / p.H, n, c0);
   const int h = static_cast<int>(item % p.H);
   const int hq = h / (p.H / p.Hg);
   const int V = p.nvt * kBV, v0 = vt * kBV;
   const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
-  const int64_t c0 = p.chunk_off[n];
   // Chunks of this sequence, bounded by the snapshots h can hold (never
   // binding for a well-formed cu_seqlens).
   const int64_t nch = max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.hcap - c0));
@@ -789,7 +791,8 @@ struct FwdH8Carry {
   float egl;   // exp(gl)
 };
 
-template <int K>
+// VN: v_new is written.
+template <int K, bool VN>
 __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
   static_assert(K == 128, "key rows of 128");
   __shared__ FwdH8Smem<K> sm;
@@ -804,12 +807,12 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
   const int vt = static_cast<int>(r % p.nvt);
   const int64_t item = (r / p.nvt) * 8 + (bid & 7);  // one XCD for the V tiles of (n, h)
   if (item >= p.N * p.H) return;
-  const int64_t n = p.seq_order[item / p.H];  // longest sequences first
+  int64_t n, c0;
+  find_ranked_seq(p, item / p.H, n, c0);  // longest sequences first
   const int h = state_head(static_cast<int>(item % p.H), p.H, p.Hg);
   const int hq = h / (p.H / p.Hg);
   const int V = p.nvt * 64, v0 = vt * 64;
   const int64_t bos = cu_at(p, n), eos = cu_at(p, n + 1);
-  const int64_t c0 = p.chunk_off[n];
   // Chunk counters are 32-bit (scalar compares; a sequence has < 2^31 chunks).
   const int nch = static_cast<int>(max<int64_t>(0, min<int64_t>((eos - bos + kC - 1) / kC, p.hcap - c0)));
 
@@ -930,8 +933,12 @@ __global__ void __launch_bounds__(kTh8) chunk_fwd_h8_kernel(FwdHParams p) {
     // The chunk's global stores are issued here, beside the state update,
     // rather than in the chain before barrier (1): 240 -> 199 us at config 4
     // on MI355X.
-    if (p.vnew && tok < L)
-      *reinterpret_cast<bf8_t*>(reinterpret_cast<bf16*>(p.vnew) + (s + tok) * vrow + vcol) = vb;
+    // Rows >= L repeat row L - 1 (their operands are clamped to it), so they
+    // store the same values there: the store is unconditional (a store that
+    // only some paths issue makes the compiler wait for every outstanding
+    // prefetch, gfx9 counting loads and stores in one counter).
+    if constexpr (VN)
+      *reinterpret_cast<bf8_t*>(reinterpret_cast<bf16*>(p.vnew) + (s + min(tok, L - 1)) * vrow + vcol) = vb;
     // Snapshot of the state entering this chunk (its bf16 hi part, still in
     // the state copy until publish_state below): lane (lg, l15) stores key
     // 32 wr + 16 t + l15, columns cb + 8 lg .. + 7.
@@ -1048,7 +1055,7 @@ chunk_fwd_o_kernel(FwdOParams p) {
   const int64_t c = blockIdx.x / p.H;
   int64_t n, s;
   int L;
-  if (!locate_chunk(p, c, n, s, L) || c >= p.hcap) return;  // block-uniform
+  if (!find_chunk(p, c, n, s, L) || c >= p.hcap) return;  // block-uniform
   const int hq = h / (p.H / p.Hg);
   const f4_t zero = {0.f, 0.f, 0.f, 0.f};
 
@@ -1176,6 +1183,7 @@ int seq_init(Seq& q, const void* cu, xk_dtype cu_dtype, int64_t N, int64_t T, vo
 // sequences into p.seq_order.
 template <class P>
 int launch_offsets(const P& p, hipStream_t s, bool order = false) {
+  if (p.N <= kWaveSeqs) return XK_OK;  // the kernels look chunks up themselves
   hipLaunchKernelGGL(chunk_offsets_kernel<P>, dim3(1), dim3(256), 0, s, p,
                      order ? p.seq_order : nullptr, nullptr, int64_t{0});
   return launch_status();
@@ -1371,8 +1379,10 @@ extern "C" int xk_chunk_fwd_h(const void* k, const void* w, const void* u, xk_dt
   if ((st = launch_offsets(p, s, true))) return st;
   const int64_t blocks = cdiv(N * H, 8) * 8 * p.nvt;
   if (blocks > INT32_MAX) return XK_ERR_UNSUPPORTED;
-  if (wide)
-    hipLaunchKernelGGL(chunk_fwd_h8_kernel<128>, dim3(static_cast<uint32_t>(blocks)), dim3(kTh8), 0, s, p);
+  if (wide && v_new)
+    hipLaunchKernelGGL((chunk_fwd_h8_kernel<128, true>), dim3(static_cast<uint32_t>(blocks)), dim3(kTh8), 0, s, p);
+  else if (wide)
+    hipLaunchKernelGGL((chunk_fwd_h8_kernel<128, false>), dim3(static_cast<uint32_t>(blocks)), dim3(kTh8), 0, s, p);
   else
     hipLaunchKernelGGL(chunk_fwd_h_kernel<128>, dim3(static_cast<uint32_t>(blocks)), dim3(kTh), 0, s, p);
   return launch_status();
