@@ -1086,6 +1086,9 @@ def measure_lib():
         lib.xkm_tail_rw.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64,
                                     ctypes.c_int64, ctypes.c_void_p]
         lib.xkm_tail_rw.restype = ctypes.c_int
+        lib.xkm_tile_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64,
+                                      ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+        lib.xkm_tile_copy.restype = ctypes.c_int
         _MEASURE = lib
     return _MEASURE
 
@@ -1140,6 +1143,36 @@ class TailFloorCase(Case):
             def run(x=x):
                 _ok(lib.xkm_tail_rw(x.data_ptr(), self.rows, self.pitch, self.tail,
                                     _cur_stream()), lib)
+            out.append(run)
+        return out
+
+
+class TileFloorCase(Case):
+    """A [rows, slices x width] array copied by tiles of 64 rows x one
+    width-byte slice, one block per tile, slices of a row group adjacent in
+    the grid: the access pattern of the chunked-GDN stage kernels (a
+    (chunk, head) piece of a [T, H, 128] bf16 tensor), as a plain copy."""
+    timing = "graph"
+    kernel = "tile_copy_kernel"
+
+    def __init__(self, rows, slices, width):
+        self.rows, self.slices, self.width = rows, slices, width
+        self.nbytes = rows * slices * width
+        self.algo_bytes = 2 * self.nbytes
+        self.name = f"tile_copy_{rows}x{slices}x{width}"
+        self.config = (f"copy of a [{rows}, {slices} x {width} B] array by 64-row x {width} B "
+                       f"tiles ({self.algo_bytes} B moved)")
+
+    def sets(self, dev, n):
+        lib = measure_lib()
+        out = []
+        for _ in range(n):
+            src = torch.empty(self.nbytes, dtype=torch.uint8, device=dev).fill_(1)
+            dst = torch.empty_like(src)
+
+            def run(src=src, dst=dst):
+                _ok(lib.xkm_tile_copy(src.data_ptr(), dst.data_ptr(), self.rows, self.slices,
+                                      self.width, _cur_stream()), lib)
             out.append(run)
         return out
 
@@ -1421,8 +1454,8 @@ PROFILE_COMMANDS = [
 # Kernels of each multi-kernel op, in launch order (per-call time against the
 # sum of their per-dispatch medians).
 OP_KERNELS = {
-    "gdn_chunk_prefill": ["chunk_offsets_kernel<ChunkParams>", "gdn_chunk_prep_kernel",
-                          "gdn_chunk_state8_kernel"],
+    # Up to 64 sequences (config 4 has 8) no offsets kernel runs.
+    "gdn_chunk_prefill": ["gdn_chunk_prep_kernel", "gdn_chunk_state8_kernel"],
 }
 
 
@@ -1700,6 +1733,17 @@ def main():
                 print(f"[bench]   stage {entry}: {sm*1e3:.2f} us, {io/1e6:.1f} MB own I/O, "
                       f"{sg / HBM_PEAK_GBS:.1%} of peak", file=sys.stderr, flush=True)
             ops[name]["stages"] = stages
+            # The same access pattern as a plain copy: [T, H, 128] bf16 moved
+            # by (chunk, head) tiles.
+            tile = TileFloorCase(case.T, case.HV, 256)
+            tus = time_gpu(tile, dev, args.steps, args.warmup, False) * 1e3
+            tgb = tile.algo_bytes / (tus * 1e-6) / 1e9
+            ops[name]["tile_copy_floor"] = {"config": tile.config, "us": round(tus, 2),
+                                            "GB/s": round(tgb, 1)}
+            for st in stages:
+                st["frac_of_tile_copy"] = round(st["GB/s"] / tgb, 4)
+            print(f"[bench]   tile-copy floor ({tile.config}): {tus:.2f} us, {tgb:.0f} GB/s",
+                  file=sys.stderr, flush=True)
         print(f"[bench] {name}: {ms*1e3:.2f} us/call, {gbs:.0f} GB/s "
               f"({gbs / HBM_PEAK_GBS:.1%} of peak)"
               + (f", {ops[name]['tokens/s']:.3g} tokens/s, "
