@@ -91,6 +91,20 @@ def test_kkt(dev, cu_list):
     torch.testing.assert_close(A[:T], ref[:T], **F32_TOL)
 
 
+@pytest.mark.parametrize("Hg,H", [(4, 4), (1, 4), (3, 6), (2, 10)])
+def test_kkt_head_groups(dev, Hg, H):
+    """GQA ratios 1, 4 and 2, and head counts that leave a partial group of
+    four (the blocks share each qk-head's key tile between its heads)."""
+    from torch_npu_ops_amd import ops
+    cu_list = [0, 70, 150]
+    _, k, _, g, beta, _, cu = _inputs(cu_list, H=Hg, HV=H, seed=4)
+    gc = og.chunk_local_cumsum(g.unsqueeze(0), cu)[0]
+    A = ops.npu_chunk_scaled_dot_kkt_fwd(_b(k, dev), _b(beta, dev), _b(gc, dev), 64,
+                                         cu.to(dev))[0].cpu()
+    ref = og.chunk_scaled_dot_kkt(k, beta, gc, cu)
+    torch.testing.assert_close(A, ref, **F32_TOL)
+
+
 @pytest.mark.parametrize("cu_list", CU_CASES)
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
 def test_solve_tril(dev, cu_list, out_dtype):
