@@ -55,6 +55,37 @@ __device__ __forceinline__ float team_sum(float v, float* red) {
   }
 }
 
+// team_sum of two values at once: one exchange through `red` (two floats
+// per wave) and two barriers instead of four.
+template <int TPG>
+__device__ __forceinline__ void team_sum2(float& a, float& b, float* red) {
+  if constexpr (TPG <= kWave) {
+    a = group_sum<TPG>(a);
+    b = group_sum<TPG>(b);
+  } else {
+    a = group_sum<kWave>(a);
+    b = group_sum<kWave>(b);
+    constexpr int kWaves = TPG / kWave;
+    const int wid = threadIdx.x / kWave;
+    const int lane = threadIdx.x % kWave;
+    __syncthreads();  // previous readers of `red` are done
+    if (lane == 0) {
+      red[2 * wid] = a;
+      red[2 * wid + 1] = b;
+    }
+    __syncthreads();
+    const int base = (threadIdx.x / TPG) * kWaves;
+    float sa = 0.f, sb = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+      sa += red[2 * (base + i)];
+      sb += red[2 * (base + i) + 1];
+    }
+    a = sa;
+    b = sb;
+  }
+}
+
 struct NormParams {
   const void* x;
   void* y;
@@ -119,7 +150,7 @@ __global__ void __launch_bounds__(TPG > 256 ? TPG : 256)
   constexpr bool kPair = VEC % 2 == 0;
   using VT = Vec<T, VEC>;
   using VW = Vec<WT, VEC>;
-  __shared__ float red[kBlock / kWave];
+  __shared__ float red[2 * (kBlock / kWave)];
 
   const int team = threadIdx.x / TPG;
   const int lane = threadIdx.x % TPG;
@@ -216,8 +247,7 @@ __global__ void __launch_bounds__(TPG > 256 ? TPG : 256)
           s2 = fmaf(f, f, s2);
         }
     }
-    s1 = team_sum<TPG>(s1, red);
-    s2 = team_sum<TPG>(s2, red);
+    team_sum2<TPG>(s1, s2, red);
     const float mean = p.is_rms ? 0.f : s1 * inv_g;
     float var = fmaxf(s2 * inv_g - mean * mean, 0.f);
     if (!p.is_rms && mean * mean > 16.f * var) {
